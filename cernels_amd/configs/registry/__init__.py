@@ -1,0 +1,166 @@
+"""The registry: every benchmarkable MoE-experts workload, keyed by name.
+
+Two families:
+
+* the five BASELINE workloads (experts only, routing precomputed on the CPU, seeded):
+  ``deepseek_v2_lite_decode_t8`` (cfg 1), ``deepseek_v2_lite_prefill`` (cfg 2),
+  ``a3b_30b_prefill`` / ``a3b_30b_decode`` (cfg 3), ``gpt_oss_20b_experts`` (cfg 4),
+  ``qwen3_next_zipf`` (cfg 5);
+* the reference's own config names and routing (src/configs/registry/*_moe_experts.py):
+  ``cohere2_moe_experts[_decode]`` (top-k of logits → sigmoid, no renorm),
+  ``deepseek_ocr2_moe_experts[_decode]`` (softmax → top-k, scale 1.0, no renorm),
+  ``gpt_oss_moe_experts`` (router inside the op call) and ``qwen3_next_moe_experts`` (router and
+  shared expert inside the op call).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from cernels_amd.configs.base import Config
+from cernels_amd.configs.modules import DenseMlp, Experts, GptOssMlp, GptOssRouter, Qwen3NextBlock, Qwen3NextRouter
+from cernels_amd.configs.synth import (
+    ACT_GPTOSS,
+    INPUT_SEED,
+    LAYOUT_INTERLEAVED,
+    ROUTER_SOFTMAX_TOPK,
+    ROUTER_SOFTMAX_TOPK_RENORM,
+    ROUTER_TOPK_SIGMOID,
+    ROUTER_TOPK_SOFTMAX,
+    WEIGHT_SEED,
+    WEIGHT_STD,
+    MoeShape,
+    make_inputs,
+    make_weights,
+)
+from cernels_amd.kops.registry import cohere2_moe_experts as _cohere2
+from cernels_amd.kops.registry import deepseek_ocr2_moe_experts as _deepseek
+from cernels_amd.kops.registry import gpt_oss_moe_experts as _gpt_oss
+from cernels_amd.kops.registry import qwen3_next_moe_experts as _qwen3
+
+_DS = dict(hidden=1280, ffn=896, experts=64, top_k=6)
+_A3B = dict(hidden=2048, ffn=768, experts=128, top_k=8)
+_GPTOSS = dict(hidden=2880, ffn=2880, experts=32, top_k=4, layout=LAYOUT_INTERLEAVED, act=ACT_GPTOSS, bias=True,
+               router=ROUTER_TOPK_SOFTMAX)
+_QWEN = dict(hidden=2048, ffn=512, experts=512, top_k=10)
+
+# BASELINE.json configs, in order.
+BASELINE_SHAPES: dict[str, MoeShape] = {
+    s.name: s
+    for s in (
+        MoeShape("deepseek_v2_lite_decode_t8", tokens=8, decode=True, **_DS),
+        MoeShape("deepseek_v2_lite_prefill", tokens=2048, **_DS),
+        MoeShape("a3b_30b_prefill", tokens=2048, **_A3B),
+        MoeShape("a3b_30b_decode", tokens=1, decode=True, **_A3B),
+        MoeShape("gpt_oss_20b_experts", tokens=4096, **_GPTOSS),
+        MoeShape("qwen3_next_zipf", tokens=4096, zipf_s=1.2, **_QWEN),
+    )
+}
+BASELINE_ORDER = list(BASELINE_SHAPES)
+HEADLINE = "deepseek_v2_lite_prefill"
+
+# The reference's configs (routing as there).
+REFERENCE_SHAPES: dict[str, MoeShape] = {
+    s.name: s
+    for s in (
+        MoeShape("cohere2_moe_experts", tokens=2048, router=ROUTER_TOPK_SIGMOID, **_A3B),
+        MoeShape("cohere2_moe_experts_decode", tokens=1, router=ROUTER_TOPK_SIGMOID, decode=True, **_A3B),
+        MoeShape("deepseek_ocr2_moe_experts", tokens=2048, router=ROUTER_SOFTMAX_TOPK, **_DS),
+        MoeShape("deepseek_ocr2_moe_experts_decode", tokens=1, router=ROUTER_SOFTMAX_TOPK, decode=True, **_DS),
+        MoeShape("gpt_oss_moe_experts", tokens=4096, **_GPTOSS),
+        MoeShape("qwen3_next_moe_experts", tokens=4096, router=ROUTER_SOFTMAX_TOPK_RENORM, **_QWEN),
+    )
+}
+
+
+def experts_module(shape: MoeShape, device) -> Experts:
+    w = make_weights(shape).to(device)
+    return Experts(w.gate_up_proj, w.down_proj, w.gate_up_proj_bias, w.down_proj_bias)
+
+
+class ExpertsConfig(Config):
+    """Experts-level workload: inputs are (x [T,H], top_k_index, top_k_weights, experts)."""
+
+    def __init__(self, shape: MoeShape, custom=None):
+        self.shape = shape
+        self.name = shape.name
+        self.op = f"routed MoE experts T={shape.tokens} H={shape.hidden} F={shape.ffn} E={shape.experts} k={shape.top_k}"
+        self.custom = custom
+
+    def inputs(self, device, dtype=torch.bfloat16):
+        if str(device) == "meta":
+            s = self.shape
+            return (torch.empty(s.tokens, s.hidden, device=device, dtype=dtype),
+                    torch.zeros(s.tokens, s.top_k, device=device, dtype=torch.int64),
+                    torch.empty(s.tokens, s.top_k, device=device, dtype=dtype), None)
+        inp = make_inputs(self.shape).to(device)
+        return inp.x, inp.top_k_index, inp.top_k_weights, experts_module(self.shape, device)
+
+
+def _seeded_normal_(module: nn.Module, seed: int = WEIGHT_SEED + 7) -> None:
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for p in module.parameters():
+            p.copy_((torch.randn(p.shape, generator=g) * WEIGHT_STD).to(p.dtype))
+
+
+class GptOssConfig(Config):
+    """Module-level gpt-oss workload (src/configs/registry/gpt_oss_moe_experts.py:23-75)."""
+
+    def __init__(self, shape: MoeShape):
+        self.shape, self.name = shape, shape.name
+        self.op = "GptOssMLP-shaped (router + clamped-SwiGLU grouped experts)"
+        self.custom = staticmethod(_gpt_oss.kernel).__func__
+
+    def inputs(self, device, dtype=torch.bfloat16):
+        s = self.shape
+        router = GptOssRouter(s.hidden, s.experts, s.top_k)
+        _seeded_normal_(router)
+        mlp = GptOssMlp(router, experts_module(s, "cpu")).to(device=device, dtype=dtype)
+        g = torch.Generator().manual_seed(INPUT_SEED)
+        x = torch.randn((1, s.tokens, s.hidden), generator=g).to(dtype).to(device)
+        return x, mlp
+
+
+class Qwen3NextConfig(Config):
+    """Module-level Qwen3-Next workload (src/configs/registry/qwen3_next_moe_experts.py:35-89)."""
+
+    shared_ffn = 512
+
+    def __init__(self, shape: MoeShape):
+        self.shape, self.name = shape, shape.name
+        self.op = "Qwen3NextSparseMoeBlock-shaped (router + grouped experts + gated shared expert)"
+        self.custom = staticmethod(_qwen3.kernel).__func__
+
+    def inputs(self, device, dtype=torch.bfloat16):
+        s = self.shape
+        gate = Qwen3NextRouter(s.hidden, s.experts, s.top_k)
+        shared = DenseMlp(s.hidden, self.shared_ffn)
+        sgate = nn.Linear(s.hidden, 1, bias=False)
+        for m in (gate, shared, sgate):
+            _seeded_normal_(m)
+        block = Qwen3NextBlock(gate, experts_module(s, "cpu"), shared, sgate).to(device=device, dtype=dtype)
+        g = torch.Generator().manual_seed(INPUT_SEED)
+        x = torch.randn((1, s.tokens, s.hidden), generator=g).to(dtype).to(device)
+        return x, block
+
+
+def _make_configs() -> dict[str, Config]:
+    cfgs: dict[str, Config] = {}
+    for name, s in BASELINE_SHAPES.items():
+        if s.layout == LAYOUT_INTERLEAVED:
+            cfgs[name] = ExpertsConfig(s, custom=None)  # experts-level gpt-oss: ops.gpt_oss_moe_experts
+        else:
+            cfgs[name] = ExpertsConfig(s, custom=_cohere2.decode_kernel if s.decode else _cohere2.kernel)
+    r = REFERENCE_SHAPES
+    cfgs["cohere2_moe_experts"] = ExpertsConfig(r["cohere2_moe_experts"], _cohere2.kernel)
+    cfgs["cohere2_moe_experts_decode"] = ExpertsConfig(r["cohere2_moe_experts_decode"], _cohere2.decode_kernel)
+    cfgs["deepseek_ocr2_moe_experts"] = ExpertsConfig(r["deepseek_ocr2_moe_experts"], _deepseek.kernel)
+    cfgs["deepseek_ocr2_moe_experts_decode"] = ExpertsConfig(r["deepseek_ocr2_moe_experts_decode"], _deepseek.decode_kernel)
+    cfgs["gpt_oss_moe_experts"] = GptOssConfig(r["gpt_oss_moe_experts"])
+    cfgs["qwen3_next_moe_experts"] = Qwen3NextConfig(r["qwen3_next_moe_experts"])
+    return cfgs
+
+
+CONFIGS: dict[str, Config] = _make_configs()

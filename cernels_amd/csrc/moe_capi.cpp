@@ -1,0 +1,233 @@
+// extern "C" entry points of libcernels_moe.so (declared in include/cernels_moe.h).
+// Argument checking, workspace carving and kernel sequencing; no device allocation, no host sync.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/cernels_moe.h"
+
+namespace cmoe {
+struct GemmParams;
+hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
+                        int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, hipStream_t stream);
+int gemm_tile_m();
+hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
+                          const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
+                          int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
+                          int32_t* sorted_pairs, int32_t* tile_expert, int max_tiles, uint16_t* glu, float* Y,
+                          hipStream_t s);
+bool decode_shape_supported(int H, int F);
+int decode_max_pairs();
+int decode_max_tokens();
+int decode_h_block();
+hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
+                         const int32_t* idx, const float* route_w, float* glu, float* Y, int32_t* tickets,
+                         uint16_t* out, int T, int H, int F, int E, int K, int act, hipStream_t s);
+}  // namespace cmoe
+
+namespace {
+
+constexpr int kMaxExperts = 1024;
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct PrefillWs {
+    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, glu, Y, total;
+    int capacity;
+};
+
+PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
+    PrefillWs w{};
+    const long long P = (long long)T * K;
+    const int bm = cmoe::gemm_tile_m();
+    w.capacity = (int)((P + bm - 1) / bm + (P < E ? P : E));
+    size_t o = 0;
+    w.offsets = o;      o = align_up(o + sizeof(int32_t) * (E + 1));
+    w.tile_offsets = o; o = align_up(o + sizeof(int32_t) * (E + 1));
+    w.meta = o;         o = align_up(o + sizeof(int32_t) * 4);
+    w.sorted_pairs = o; o = align_up(o + sizeof(int32_t) * P);
+    w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
+    w.glu = o;          o = align_up(o + sizeof(uint16_t) * P * F);
+    w.Y = o;            o = align_up(o + sizeof(float) * P * H);
+    w.total = o;
+    return w;
+}
+
+struct DecodeWs {
+    size_t glu, Y, tickets, total;
+};
+
+DecodeWs decode_ws(int T, int H, int F, int K) {
+    DecodeWs w{};
+    const long long P = (long long)T * K;
+    size_t o = 0;
+    w.glu = o;     o = align_up(o + sizeof(float) * P * F);
+    w.Y = o;       o = align_up(o + sizeof(float) * P * H);
+    w.tickets = o; o = align_up(o + sizeof(int32_t) * ((H + cmoe::decode_h_block() - 1) / cmoe::decode_h_block()));
+    w.total = o;
+    return w;
+}
+
+bool dims_ok(int T, int H, int F, int E, int K) {
+    return T >= 0 && H > 0 && F > 0 && E > 0 && K > 0 && (long long)T * K < (1LL << 31);
+}
+
+int common_checks(const void* x, const void* w1, const void* w2, const int32_t* idx, const float* wts, int T,
+                  int H, int F, int E, int K, int layout, int act, void* out, void* ws) {
+    if (!dims_ok(T, H, F, E, K)) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (layout != CERNELS_MOE_LAYOUT_CONCAT && layout != CERNELS_MOE_LAYOUT_INTERLEAVED)
+        return CERNELS_MOE_INVALID_ARGUMENT;
+    if (act != CERNELS_MOE_ACT_SILU && act != CERNELS_MOE_ACT_GPTOSS) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (T == 0) return CERNELS_MOE_OK;
+    if (!x || !w1 || !w2 || !idx || !wts || !out || !ws) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || !aligned16(out) || !aligned16(ws))
+        return CERNELS_MOE_MISALIGNED;
+    if ((reinterpret_cast<uintptr_t>(idx) & 3u) || (reinterpret_cast<uintptr_t>(wts) & 3u))
+        return CERNELS_MOE_MISALIGNED;
+    return CERNELS_MOE_OK;
+}
+
+int hip_status(hipError_t e) { return e == hipSuccess ? CERNELS_MOE_OK : CERNELS_MOE_HIP_ERROR; }
+
+}  // namespace
+
+extern "C" {
+
+const char* cernels_moe_version(void) { return "cernels_moe 0.1 gfx950"; }
+
+const char* cernels_moe_status_string(int status) {
+    switch (status) {
+        case CERNELS_MOE_OK: return "ok";
+        case CERNELS_MOE_INVALID_ARGUMENT: return "invalid argument";
+        case CERNELS_MOE_UNSUPPORTED_SHAPE: return "unsupported shape";
+        case CERNELS_MOE_MISALIGNED: return "tensor pointer not 16-byte aligned";
+        case CERNELS_MOE_WORKSPACE_TOO_SMALL: return "workspace too small";
+        case CERNELS_MOE_HIP_ERROR: return "HIP kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t tile_m) {
+    if (T < 0 || K <= 0 || E <= 0 || tile_m <= 0) return 0;
+    const long long P = (long long)T * K;
+    const long long cap = (P + tile_m - 1) / tile_m + (P < E ? P : E);
+    return (size_t)(cap > 0 ? cap : 1);
+}
+
+int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, int32_t tile_m,
+                      int32_t* expert_offsets, int32_t* sorted_pairs, int32_t* tile_offsets, int32_t* tile_expert,
+                      int32_t* meta, hipStream_t stream) {
+    if (T < 0 || K <= 0 || E <= 0 || E > kMaxExperts || tile_m <= 0 || (long long)T * K >= (1LL << 31))
+        return CERNELS_MOE_INVALID_ARGUMENT;
+    if (!expert_offsets || !tile_offsets || !tile_expert || !meta) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (T > 0 && (!indices || !sorted_pairs)) return CERNELS_MOE_INVALID_ARGUMENT;
+    return hip_status(cmoe::launch_route(indices, T, K, E, tile_m, expert_offsets, sorted_pairs, tile_offsets,
+                                         tile_expert, meta, stream));
+}
+
+size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K) {
+    if (!dims_ok(T, H, F, E, K)) return 0;
+    return prefill_ws(T, H, F, E, K).total;
+}
+
+int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias, const void* down_proj,
+                        const float* down_bias, const int32_t* indices, const float* weights, int32_t T, int32_t H,
+                        int32_t F, int32_t E, int32_t K, int32_t layout, int32_t act, void* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+    int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
+    if (st != CERNELS_MOE_OK || T == 0) return st;
+    if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    const PrefillWs w = prefill_ws(T, H, F, E, K);
+    if (workspace_bytes < w.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
+    char* base = static_cast<char*>(workspace);
+    return hip_status(cmoe::launch_prefill(
+        x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, T, H, F, E, K, layout, act, out,
+        reinterpret_cast<int32_t*>(base + w.offsets), reinterpret_cast<int32_t*>(base + w.tile_offsets),
+        reinterpret_cast<int32_t*>(base + w.meta), reinterpret_cast<int32_t*>(base + w.sorted_pairs),
+        reinterpret_cast<int32_t*>(base + w.tile_expert), w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
+        reinterpret_cast<float*>(base + w.Y), stream));
+}
+
+int32_t cernels_moe_decode_max_tokens(void) { return cmoe::decode_max_tokens(); }
+int32_t cernels_moe_decode_max_pairs(void) { return cmoe::decode_max_pairs(); }
+
+size_t cernels_moe_experts_decode_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K) {
+    if (!dims_ok(T, H, F, E, K)) return 0;
+    return decode_ws(T, H, F, K).total;
+}
+
+int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                               const void* down_proj, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+    int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
+    if (st != CERNELS_MOE_OK || T == 0) return st;
+    if (layout != CERNELS_MOE_LAYOUT_CONCAT) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (T > cmoe::decode_max_tokens() || T * K > cmoe::decode_max_pairs()) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (H % 8 || F % 8 || !cmoe::decode_shape_supported(H, F)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    const DecodeWs w = decode_ws(T, H, F, K);
+    if (workspace_bytes < w.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
+    char* base = static_cast<char*>(workspace);
+    return hip_status(cmoe::launch_decode(
+        static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(gate_up_proj), gate_up_bias,
+        static_cast<const uint16_t*>(down_proj), down_bias, indices, weights, reinterpret_cast<float*>(base + w.glu),
+        reinterpret_cast<float*>(base + w.Y), reinterpret_cast<int32_t*>(base + w.tickets),
+        static_cast<uint16_t*>(out), T, H, F, E, K, act, stream));
+}
+
+// ---- the reference's per-model ops ----------------------------------------------------------------
+
+int cernels_cohere2_moe_experts(const void* x, const void* gate_up_proj, const void* down_proj, const int32_t* indices,
+                                const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t topk,
+                                void* out, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return cernels_moe_experts(x, gate_up_proj, nullptr, down_proj, nullptr, indices, weights, T, H, F, E, topk,
+                               CERNELS_MOE_LAYOUT_CONCAT, CERNELS_MOE_ACT_SILU, out, workspace, workspace_bytes,
+                               stream);
+}
+
+int cernels_cohere2_moe_experts_decode(const void* x, const void* gate_up_proj, const void* down_proj,
+                                       const int32_t* indices, const float* weights, int32_t T, int32_t H, int32_t F,
+                                       int32_t E, int32_t topk, void* out, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+    return cernels_moe_experts_decode(x, gate_up_proj, nullptr, down_proj, nullptr, indices, weights, T, H, F, E,
+                                      topk, CERNELS_MOE_LAYOUT_CONCAT, CERNELS_MOE_ACT_SILU, out, workspace,
+                                      workspace_bytes, stream);
+}
+
+int cernels_deepseek_ocr2_moe_experts(const void* x, const void* gate_up_proj, const void* down_proj,
+                                      const int32_t* indices, const float* weights, int32_t T, int32_t H, int32_t F,
+                                      int32_t E, int32_t topk, void* out, void* workspace, size_t workspace_bytes,
+                                      hipStream_t stream) {
+    return cernels_cohere2_moe_experts(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, topk, out, workspace,
+                                       workspace_bytes, stream);
+}
+
+int cernels_deepseek_ocr2_moe_experts_decode(const void* x, const void* gate_up_proj, const void* down_proj,
+                                             const int32_t* indices, const float* weights, int32_t T, int32_t H,
+                                             int32_t F, int32_t E, int32_t topk, void* out, void* workspace,
+                                             size_t workspace_bytes, hipStream_t stream) {
+    return cernels_cohere2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, topk, out,
+                                              workspace, workspace_bytes, stream);
+}
+
+int cernels_qwen3_next_moe_experts(const void* x, const void* gate_up_proj, const void* down_proj,
+                                   const int32_t* indices, const float* weights, int32_t T, int32_t H, int32_t F,
+                                   int32_t E, int32_t topk, void* out, void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+    return cernels_cohere2_moe_experts(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, topk, out, workspace,
+                                       workspace_bytes, stream);
+}
+
+int cernels_gpt_oss_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                                const void* down_proj, const float* down_bias, const int32_t* indices,
+                                const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t topk,
+                                void* out, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    return cernels_moe_experts(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, T, H, F, E,
+                               topk, CERNELS_MOE_LAYOUT_INTERLEAVED, CERNELS_MOE_ACT_GPTOSS, out, workspace,
+                               workspace_bytes, stream);
+}
+
+}  // extern "C"

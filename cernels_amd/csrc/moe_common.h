@@ -1,0 +1,65 @@
+// Shared definitions for the gfx950 routed-MoE-experts kernels.
+//
+// Conventions used across the kernels:
+//   T tokens, H hidden, F expert intermediate, E experts, K top-k, P = T*K routed pairs.
+//   A "pair" p = t*K + k is one (token, top-k slot) entry of top_k_index[T, K].
+//   Pairs are grouped by expert in op_eager order: expert ascending, then slot k, then token t
+//   (transformers Cohere2MoeExperts.forward: torch.where over the [K, T] one-hot slice,
+//   modeling_cohere2_moe.py:122-130).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cmoe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// Weight layouts (mirrors include/cernels_moe.h).
+constexpr int kLayoutConcat = 0;       // gate_up [E, 2F, H] (gate rows, then up rows), down [E, H, F]
+constexpr int kLayoutInterleaved = 1;  // gate_up [E, H, 2F] (even col gate, odd col up), down [E, F, H]
+// Activations.
+constexpr int kActSilu = 0;    // silu(gate) * up
+constexpr int kActGptOss = 1;  // (clamp(up,-7,7) + 1) * g * sigmoid(1.702 g), g = min(gate, 7)
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 bits (same rounding torch uses for .to(bfloat16)).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    __bf16 b = (__bf16)f;
+    return __builtin_bit_cast(uint16_t, b);
+}
+
+// SwiGLU variants in fp32.
+//   silu:   transformers ACT2FN["silu"] = x * sigmoid(x)  (modeling_cohere2_moe.py:131)
+//   gpt-oss: GptOssExperts._apply_gate (modeling_gpt_oss.py:82-88), alpha 1.702, limit 7.0
+template <int ACT>
+__device__ __forceinline__ float swiglu(float gate, float up) {
+    if constexpr (ACT == kActSilu) {
+        return gate / (1.0f + __expf(-gate)) * up;
+    } else {
+        gate = fminf(gate, 7.0f);
+        up = fminf(fmaxf(up, -7.0f), 7.0f);
+        float glu = gate / (1.0f + __expf(-1.702f * gate));
+        return (up + 1.0f) * glu;
+    }
+}
+
+// Full-wave (64-lane) sum; every lane returns the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace cmoe

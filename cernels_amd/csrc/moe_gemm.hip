@@ -1,0 +1,401 @@
+// Prefill grouped GEMMs for the routed experts, bf16 MFMA on gfx950.
+//
+//   GEMM1  glu[r, :]  = act( X[tok(r), :] · W1_e^T )   rows r of expert e, SwiGLU in the epilogue
+//   GEMM2  Y[p, :]    = w_p · ( glu[r, :] · W2_e^T + b2_e )   written at the pair's own row p
+//   combine out[t, :] = bf16( sum_k Y[t*K + k, :] )
+//
+// Replaces the reference's per-expert host loop (src/kops/cohere2_moe_experts/csrc/
+// cohere2_moe_experts.cu:315-358: gather_kernel, cublasGemmEx x2, swiglu_kernel,
+// scatter_add_f32_kernel, final cast; gpt-oss adds add_gateup_bias_kernel,
+// src/kops/gpt_oss_moe_experts/csrc/gpt_oss_moe_experts.cu:75-117). Here the gather is folded
+// into GEMM1's operand load, the SwiGLU (and the gpt-oss gate_up bias) into GEMM1's epilogue,
+// the down bias and routing weight into GEMM2's epilogue, and no host synchronisation is needed:
+// the GEMMs read the tile list the route kernel left in device memory.
+//
+// Scheduling: a persistent grid (a multiple of 8 workgroups). Work items are (expert, N-tile,
+// M-tile) in expert-major order, M fastest, so the M-tiles that share one weight tile are
+// neighbours. Workgroup b runs on XCD b % 8; item range [x*per, (x+1)*per) is given to XCD x so
+// that neighbours share that XCD's L2 and each weight tile is fetched from HBM about once.
+//
+// Tile: 128 rows x 128 B-rows x 64 K per step, 256 threads = 4 waves (2 x 2), each wave a
+// 64 x 64 block of v_mfma_f32_32x32x16_bf16. A and B tiles are staged through LDS with a
+// register double buffer; 16-byte chunks are XOR-swizzled by (row & 7) against bank conflicts.
+// GEMM1's B tile holds 64 gate rows then the 64 matching up rows, so one lane owns the gate and
+// the up value of the same output column and the SwiGLU happens in registers.
+#include "moe_common.h"
+
+namespace cmoe {
+
+constexpr int kBM = 128;
+constexpr int kBN = 128;  // B-tile rows (GEMM1: 64 gate + 64 up -> 64 glu columns)
+constexpr int kBK = 64;
+constexpr int kGemmThreads = 256;
+constexpr int kTileBytes = kBM * kBK * 2;  // 16 KB, A and B alike
+
+// Kernel modes.
+constexpr int kModeGateUp = 0;
+constexpr int kModeDown = 1;
+
+struct GemmParams {
+    const uint16_t* A;             // GEMM1: x [T, H]; GEMM2: glu [P, F] (rows in expert order)
+    const uint16_t* B;             // expert weights, expert 0
+    const float* bias;             // GEMM1: [E, 2F]; GEMM2: [E, H]; or null
+    const int32_t* sorted_pairs;   // [P] pair id per expert-ordered row
+    const int32_t* offsets;        // [E+1]
+    const int32_t* tile_offsets;   // [E+1]
+    const int32_t* tile_expert;    // [tiles]
+    const int32_t* meta;           // [0] = tiles
+    const float* route_w;          // [P] fp32 routing weight per pair (GEMM2)
+    void* out;                     // GEMM1: glu bf16 [P, F]; GEMM2: Y fp32 [P, H]
+    int Kdim;                      // reduction length: H (GEMM1) or F (GEMM2)
+    int N;                         // output columns: F (GEMM1) or H (GEMM2)
+    int F;                         // expert intermediate size
+    int topk;
+    int n_tiles;                   // output column tiles
+    long long expert_stride;       // elements of one expert's matrix in B
+    int ldb;                       // row stride of B (elements)
+};
+
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * (kBK * 2) + ((chunk ^ (row & 7)) << 4); }
+
+__device__ __forceinline__ u32x4 ld_global_16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Transposes 4 K-rows x 8 columns of bf16 (v[i] = row i) into 8 columns x 4 K (two dwords each).
+__device__ __forceinline__ void transpose_4x8(const u32x4 (&v)[4], u32x2 (&o)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int d = j >> 1;
+        uint32_t a0 = v[0][d], a1 = v[1][d], a2 = v[2][d], a3 = v[3][d];
+        if (j & 1) {
+            o[j][0] = (a0 >> 16) | (a1 & 0xffff0000u);
+            o[j][1] = (a2 >> 16) | (a3 & 0xffff0000u);
+        } else {
+            o[j][0] = (a0 & 0xffffu) | (a1 << 16);
+            o[j][1] = (a2 & 0xffffu) | (a3 << 16);
+        }
+    }
+}
+
+template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
+__global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams prm) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    // LDS: A buffers 0,1 then B buffers 0,1, one 16 KB tile each
+    auto ldsA = [&](int buf) { return smem + buf * kTileBytes; };
+    auto ldsB = [&](int buf) { return smem + (2 + buf) * kTileBytes; };
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int wm = wave & 1, wn = wave >> 1;
+    constexpr bool kBNcontig = (LAYOUT == kLayoutInterleaved);
+
+    const int tiles = prm.meta[0];
+    const int total = tiles * prm.n_tiles;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
+    const int per = ceil_div(total, 8);
+    const int it_end = min(total, (xcd + 1) * per);
+
+    for (int it = xcd * per + slot; it < it_end; it += slots) {
+        // ---- item -> (expert, n-tile, m-tile)
+        const int e = prm.tile_expert[it / prm.n_tiles];
+        const int t0 = prm.tile_offsets[e], nt_e = prm.tile_offsets[e + 1] - t0;
+        const int local = it - t0 * prm.n_tiles;
+        const int n_idx = local / nt_e, m_idx = local - n_idx * nt_e;
+        const int seg0 = prm.offsets[e], seg_n = prm.offsets[e + 1] - seg0;
+        const int row_begin = seg0 + m_idx * kBM;
+        const int rows = min(kBM, seg_n - m_idx * kBM);
+        const int n0 = n_idx * (MODE == kModeGateUp ? kBN / 2 : kBN);  // first output column
+        const uint16_t* Be = prm.B + (long long)e * prm.expert_stride;
+        const int Kd = prm.Kdim;
+
+        // ---- per-thread global source pointers for A (4 rows) and B
+        const int ac = tid & 7;
+        const uint16_t* a_src[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = min((tid >> 3) + 32 * i, rows - 1);
+            long long src_row;
+            if constexpr (MODE == kModeGateUp) src_row = prm.sorted_pairs[row_begin + r] / prm.topk;
+            else src_row = row_begin + r;
+            a_src[i] = prm.A + src_row * Kd + ac * 8;
+        }
+        const uint16_t* b_src[4];
+        if constexpr (!kBNcontig) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = (tid >> 3) + 32 * i;  // B-tile row
+                int wrow;
+                if constexpr (MODE == kModeGateUp) {
+                    const int c = min(n0 + (r & 63), prm.F - 1);
+                    wrow = r < 64 ? c : prm.F + c;
+                } else {
+                    wrow = min(n0 + r, prm.N - 1);
+                }
+                b_src[i] = Be + (long long)wrow * prm.ldb + ac * 8;
+            }
+        } else {
+            // 4 K-rows x 8 columns per thread; columns of W [K, ncols]
+            const int ng = tid & 15, kg = tid >> 4;
+            const int ncols = (MODE == kModeGateUp) ? 2 * prm.F : prm.N;
+            int col = (MODE == kModeGateUp ? 2 * n0 : n0) + ng * 8;
+            if (col + 8 > ncols) col = (MODE == kModeGateUp ? 2 * n0 : n0);  // tail: any valid column
+#pragma unroll
+            for (int i = 0; i < 4; ++i) b_src[i] = Be + (long long)(kg * 4 + i) * prm.ldb + col;
+        }
+
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+        u32x4 ra[4], rb[4];
+        auto load_regs = [&](int kt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ra[i] = ld_global_16(a_src[i] + kt * kBK);
+            if constexpr (!kBNcontig) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + kt * kBK);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + (long long)kt * kBK * prm.ldb);
+            }
+        };
+        auto store_lds = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<u32x4*>(ldsA(buf) + lds_off((tid >> 3) + 32 * i, ac)) = ra[i];
+            if constexpr (!kBNcontig) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    *reinterpret_cast<u32x4*>(ldsB(buf) + lds_off((tid >> 3) + 32 * i, ac)) = rb[i];
+            } else {
+                u32x2 o[8];
+                transpose_4x8(rb, o);
+                const int ng = tid & 15, kg = tid >> 4;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int nl = ng * 8 + j;
+                    int lrow;
+                    if constexpr (MODE == kModeGateUp) lrow = (nl & 1) ? 64 + (nl >> 1) : (nl >> 1);
+                    else lrow = nl;
+                    *reinterpret_cast<u32x2*>(ldsB(buf) + lds_off(lrow, kg >> 1) + (kg & 1) * 8) = o[j];
+                }
+            }
+        };
+
+        // B-tile rows used by this wave for its two 32-column blocks
+        int brow[2];
+        if constexpr (MODE == kModeGateUp) {
+            brow[0] = wn * 32;       // gate
+            brow[1] = 64 + wn * 32;  // up
+        } else {
+            brow[0] = wn * 64;
+            brow[1] = wn * 64 + 32;
+        }
+        const int arow0 = wm * 64 + (lane & 31);
+        const int khalf = lane >> 5;
+
+        const int nk = Kd / kBK;
+        load_regs(0);
+        store_lds(0);
+        __syncthreads();
+        for (int kt = 0; kt < nk; ++kt) {
+            const int buf = kt & 1;
+            if (kt + 1 < nk) load_regs(kt + 1);
+#pragma unroll
+            for (int ks = 0; ks < kBK / 16; ++ks) {
+                const int chunk = ks * 2 + khalf;
+                bf16x8 af[2], bfr[2];
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    af[mb] = *reinterpret_cast<const bf16x8*>(ldsA(buf) + lds_off(arow0 + mb * 32, chunk));
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    bfr[nb] = *reinterpret_cast<const bf16x8*>(ldsB(buf) + lds_off(brow[nb] + (lane & 31), chunk));
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], bfr[nb], acc[mb][nb], 0, 0, 0);
+            }
+            if (kt + 1 < nk) store_lds(buf ^ 1);
+            __syncthreads();
+        }
+
+        // ---- epilogue. Output lane layout of the 32x32 block: column = lane & 31,
+        // row = 8*(r/4) + 4*(lane/32) + (r%4) for accumulator element r.
+        if constexpr (MODE == kModeGateUp) {
+            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+            const int n = n0 + wn * 32 + (lane & 31);
+            if (n < prm.N) {
+                float bg = 0.f, bu = 0.f;
+                if constexpr (HAS_BIAS) {
+                    const float* be = prm.bias + (long long)e * 2 * prm.F;
+                    bg = LAYOUT == kLayoutInterleaved ? be[2 * n] : be[n];
+                    bu = LAYOUT == kLayoutInterleaved ? be[2 * n + 1] : be[prm.F + n];
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < rows) {
+                            const float v = swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu);
+                            glu[(long long)(row_begin + row) * prm.F + n] = f32_to_bf16_bits(v);
+                        }
+                    }
+            }
+        } else {
+            float* Y = reinterpret_cast<float*>(prm.out);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < rows) {
+                        const int p = prm.sorted_pairs[row_begin + row];
+                        const float w = prm.route_w[p];
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb) {
+                            const int n = n0 + brow[nb] + (lane & 31);
+                            if (n < prm.N) {
+                                float v = acc[mb][nb][r];
+                                if constexpr (HAS_BIAS) v += prm.bias[(long long)e * prm.N + n];
+                                Y[(long long)p * prm.N + n] = v * w;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();  // LDS reuse by the next item
+    }
+}
+
+// out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] ), slots in k order.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ Y, const int32_t* __restrict__ idx,
+                                                          uint16_t* __restrict__ out, int T, int K, int E, int H) {
+    const int t = blockIdx.x;
+    const int ncol4 = H / 4;
+    for (int c = threadIdx.x; c < ncol4; c += blockDim.x) {
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < K; ++k) {
+            const int e = idx[t * K + k];
+            if ((unsigned)e >= (unsigned)E) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(Y + ((long long)t * K + k) * H + 4 * c);
+            s += v;
+        }
+        u32x2 o;
+        o[0] = (uint32_t)f32_to_bf16_bits(s[0]) | ((uint32_t)f32_to_bf16_bits(s[1]) << 16);
+        o[1] = (uint32_t)f32_to_bf16_bits(s[2]) | ((uint32_t)f32_to_bf16_bits(s[3]) << 16);
+        *reinterpret_cast<u32x2*>(out + (long long)t * H + 4 * c) = o;
+    }
+}
+
+static int g_cu_count = 0;
+
+static int cu_count() {
+    if (g_cu_count == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_cu_count = n;
+        else
+            g_cu_count = 256;
+    }
+    return g_cu_count;
+}
+
+int gemm_tile_m() { return kBM; }
+
+template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
+static hipError_t launch_gemm_t(const GemmParams& prm, int max_tiles, hipStream_t stream) {
+    const int upper = max_tiles * prm.n_tiles;
+    int grid = min(upper, cu_count() * 2);
+    grid = ceil_div(max(grid, 1), 8) * 8;
+    const size_t lds = 4 * (size_t)kTileBytes;
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>), dim3(grid), dim3(kGemmThreads), lds, stream,
+                       prm);
+    return hipGetLastError();
+}
+
+hipError_t launch_gateup(const GemmParams& prm, int layout, int act, bool has_bias, int max_tiles, hipStream_t s) {
+    if (layout == kLayoutConcat) {
+        if (act == kActSilu)
+            return has_bias ? launch_gemm_t<kModeGateUp, kLayoutConcat, kActSilu, true>(prm, max_tiles, s)
+                            : launch_gemm_t<kModeGateUp, kLayoutConcat, kActSilu, false>(prm, max_tiles, s);
+        return has_bias ? launch_gemm_t<kModeGateUp, kLayoutConcat, kActGptOss, true>(prm, max_tiles, s)
+                        : launch_gemm_t<kModeGateUp, kLayoutConcat, kActGptOss, false>(prm, max_tiles, s);
+    }
+    if (act == kActSilu)
+        return has_bias ? launch_gemm_t<kModeGateUp, kLayoutInterleaved, kActSilu, true>(prm, max_tiles, s)
+                        : launch_gemm_t<kModeGateUp, kLayoutInterleaved, kActSilu, false>(prm, max_tiles, s);
+    return has_bias ? launch_gemm_t<kModeGateUp, kLayoutInterleaved, kActGptOss, true>(prm, max_tiles, s)
+                    : launch_gemm_t<kModeGateUp, kLayoutInterleaved, kActGptOss, false>(prm, max_tiles, s);
+}
+
+hipError_t launch_down(const GemmParams& prm, int layout, bool has_bias, int max_tiles, hipStream_t s) {
+    if (layout == kLayoutConcat)
+        return has_bias ? launch_gemm_t<kModeDown, kLayoutConcat, kActSilu, true>(prm, max_tiles, s)
+                        : launch_gemm_t<kModeDown, kLayoutConcat, kActSilu, false>(prm, max_tiles, s);
+    return has_bias ? launch_gemm_t<kModeDown, kLayoutInterleaved, kActSilu, true>(prm, max_tiles, s)
+                    : launch_gemm_t<kModeDown, kLayoutInterleaved, kActSilu, false>(prm, max_tiles, s);
+}
+
+hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
+                          hipStream_t s) {
+    if (T == 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, s, Y, idx, out, T, K, E, H);
+    return hipGetLastError();
+}
+
+hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
+                        int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, hipStream_t stream);
+
+// route -> gate_up GEMM -> down GEMM -> combine, all on stream s. Shapes were checked by the caller
+// (H % 64 == 0, F % 64 == 0, E <= 1024, T >= 1).
+hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
+                          const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
+                          int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
+                          int32_t* sorted_pairs, int32_t* tile_expert, int max_tiles, uint16_t* glu, float* Y,
+                          hipStream_t s) {
+    hipError_t st = launch_route(idx, T, K, E, kBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, s);
+    if (st != hipSuccess) return st;
+    const bool concat = layout == kLayoutConcat;
+    GemmParams g1{};
+    g1.A = static_cast<const uint16_t*>(x);
+    g1.B = static_cast<const uint16_t*>(w1);
+    g1.bias = b1;
+    g1.sorted_pairs = sorted_pairs;
+    g1.offsets = offsets;
+    g1.tile_offsets = tile_offsets;
+    g1.tile_expert = tile_expert;
+    g1.meta = meta;
+    g1.route_w = route_w;
+    g1.out = glu;
+    g1.Kdim = H;
+    g1.N = F;
+    g1.F = F;
+    g1.topk = K;
+    g1.n_tiles = ceil_div(F, kBN / 2);
+    g1.expert_stride = 2LL * F * H;
+    g1.ldb = concat ? H : 2 * F;
+    st = launch_gateup(g1, layout, act, b1 != nullptr, max_tiles, s);
+    if (st != hipSuccess) return st;
+    GemmParams g2 = g1;
+    g2.A = glu;
+    g2.B = static_cast<const uint16_t*>(w2);
+    g2.bias = b2;
+    g2.out = Y;
+    g2.Kdim = F;
+    g2.N = H;
+    g2.n_tiles = ceil_div(H, kBN);
+    g2.expert_stride = (long long)H * F;
+    g2.ldb = concat ? F : H;
+    st = launch_down(g2, layout, b2 != nullptr, max_tiles, s);
+    if (st != hipSuccess) return st;
+    return launch_combine(Y, idx, static_cast<uint16_t*>(out), T, K, E, H, s);
+}
+
+}  // namespace cmoe

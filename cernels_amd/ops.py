@@ -1,0 +1,175 @@
+"""Torch-facing MoE-experts ops over the C ABI (libcernels_moe.so).
+
+Same names, argument order and error behaviour as the reference's torch ops
+(src/kops/<slug>/torch-ext/torch_binding.cpp; C++ checks in csrc/<slug>.cu, e.g.
+cohere2_moe_experts.cu:253-257 and :213-216): inputs must be contiguous CUDA tensors,
+``x`` / expert weights bf16, ``indices`` int32, ``weights`` fp32 (gpt-oss biases fp32); a
+violated contract raises ``RuntimeError``. Output is a new bf16 ``[T, H]`` tensor. Kernels run on
+the current HIP stream of ``x``'s device, with no host synchronisation.
+
+Scratch memory comes from torch's caching allocator and is handed to the library as a workspace.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from cernels_amd import _native
+from cernels_amd._native import ACT_GPTOSS, ACT_SILU, LAYOUT_CONCAT, LAYOUT_INTERLEAVED, check
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_inputs(x, gate_up_proj, down_proj, indices, weights, topk, layout, gate_up_bias=None, down_bias=None):
+    tensors = [x, gate_up_proj, down_proj, indices, weights] + [t for t in (gate_up_bias, down_bias) if t is not None]
+    _require(all(isinstance(t, torch.Tensor) for t in tensors), "inputs must be tensors")
+    _require(all(t.is_cuda for t in tensors), "all inputs must be CUDA (HIP) tensors")
+    _require(all(t.device == x.device for t in tensors), "all inputs must be on the same device")
+    _require(all(t.is_contiguous() for t in tensors), "all inputs must be contiguous")
+    _require(x.dtype == torch.bfloat16, "x must be bfloat16")
+    _require(gate_up_proj.dtype == torch.bfloat16 and down_proj.dtype == torch.bfloat16, "expert weights must be bfloat16")
+    _require(indices.dtype == torch.int32, "indices must be int32")
+    _require(weights.dtype == torch.float32, "weights must be float32")
+    _require(x.dim() == 2 and gate_up_proj.dim() == 3 and down_proj.dim() == 3, "x must be [T, H], weights [E, ., .]")
+    T, H = x.shape
+    E = gate_up_proj.size(0)
+    if layout == LAYOUT_CONCAT:
+        _require(gate_up_proj.size(2) == H and gate_up_proj.size(1) % 2 == 0, "gate_up_proj must be [E, 2F, H]")
+        F = gate_up_proj.size(1) // 2
+        _require(tuple(down_proj.shape) == (E, H, F), "down_proj must be [E, H, F]")
+    else:
+        _require(gate_up_proj.size(1) == H and gate_up_proj.size(2) % 2 == 0, "gate_up_proj must be [E, H, 2F]")
+        F = gate_up_proj.size(2) // 2
+        _require(tuple(down_proj.shape) == (E, F, H), "down_proj must be [E, F, H]")
+    _require(tuple(indices.shape) == (T, int(topk)), "indices must be [T, topk]")
+    _require(tuple(weights.shape) == (T, int(topk)), "weights must be [T, topk]")
+    if gate_up_bias is not None:
+        _require(gate_up_bias.dtype == torch.float32 and tuple(gate_up_bias.shape) == (E, 2 * F), "gate_up_bias must be fp32 [E, 2F]")
+    if down_bias is not None:
+        _require(down_bias.dtype == torch.float32 and tuple(down_bias.shape) == (E, H), "down_bias must be fp32 [E, H]")
+    return int(T), int(H), int(F), int(E)
+
+
+def moe_experts(
+    x: torch.Tensor,
+    gate_up_proj: torch.Tensor,
+    down_proj: torch.Tensor,
+    indices: torch.Tensor,
+    weights: torch.Tensor,
+    topk: int,
+    *,
+    layout: int = LAYOUT_CONCAT,
+    act: int = ACT_SILU,
+    gate_up_bias: torch.Tensor | None = None,
+    down_bias: torch.Tensor | None = None,
+    decode: bool = False,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Routed experts forward through the native library (prefill grouped GEMM or decode GEMV)."""
+    T, H, F, E = _check_inputs(x, gate_up_proj, down_proj, indices, weights, topk, layout, gate_up_bias, down_bias)
+    K = int(topk)
+    L = _native.lib()
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
+    else:
+        _require(out.is_contiguous() and out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H), "bad out tensor")
+    if T == 0:
+        return out
+    with torch.cuda.device(x.device):
+        if decode:
+            nbytes = L.cernels_moe_experts_decode_workspace_bytes(T, H, F, E, K)
+            fn, name = L.cernels_moe_experts_decode, "cernels_moe_experts_decode"
+        else:
+            nbytes = L.cernels_moe_experts_workspace_bytes(T, H, F, E, K)
+            fn, name = L.cernels_moe_experts, "cernels_moe_experts"
+        _require(nbytes > 0, f"{name}: invalid dimensions T={T} H={H} F={F} E={E} K={K}")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        st = fn(
+            _ptr(x), _ptr(gate_up_proj), _ptr(gate_up_bias), _ptr(down_proj), _ptr(down_bias), _ptr(indices),
+            _ptr(weights), T, H, F, E, K, layout, act, _ptr(out), _ptr(ws), ctypes.c_size_t(nbytes),
+            _stream(x.device),
+        )
+        check(st, name)
+    return out
+
+
+def decode_supported(T: int, K: int, H: int, F: int, layout: int = LAYOUT_CONCAT) -> bool:
+    """True if the decode entry accepts this shape (otherwise use the prefill entry)."""
+    L = _native.lib()
+    return (
+        layout == LAYOUT_CONCAT
+        and 1 <= T <= L.cernels_moe_decode_max_tokens()
+        and T * K <= L.cernels_moe_decode_max_pairs()
+        and H % 8 == 0 and F % 8 == 0 and H <= 4096 and F <= 4096
+    )
+
+
+def route(indices: torch.Tensor, num_experts: int, tile_m: int = 128):
+    """Device routing only: (expert_offsets [E+1], sorted_pairs [T*K], tile_offsets [E+1],
+    tile_expert [capacity], meta [2]) — the tensors the prefill GEMMs schedule from."""
+    _require(indices.is_cuda and indices.dtype == torch.int32 and indices.is_contiguous() and indices.dim() == 2,
+             "indices must be a contiguous int32 CUDA tensor [T, K]")
+    T, K = map(int, indices.shape)
+    L = _native.lib()
+    cap = L.cernels_moe_route_tile_capacity(T, K, num_experts, tile_m)
+    dev = indices.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, **i32)
+    pairs = torch.full((max(T * K, 1),), -1, **i32)
+    toff = torch.empty(num_experts + 1, **i32)
+    texp = torch.full((max(cap, 1),), -1, **i32)
+    meta = torch.empty(2, **i32)
+    with torch.cuda.device(dev):
+        st = L.cernels_moe_route(_ptr(indices), T, K, num_experts, tile_m, _ptr(offsets), _ptr(pairs), _ptr(toff),
+                                 _ptr(texp), _ptr(meta), _stream(dev))
+    check(st, "cernels_moe_route")
+    return offsets, pairs[: T * K], toff, texp, meta
+
+
+# ---- the reference's per-model torch ops (same schemas) ---------------------------------------
+
+def cohere2_moe_experts(x, gate_up_proj, down_proj, indices, weights, topk):
+    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk)
+
+
+def cohere2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weights, topk):
+    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk, decode=True)
+
+
+def deepseek_ocr2_moe_experts(x, gate_up_proj, down_proj, indices, weights, topk):
+    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk)
+
+
+def deepseek_ocr2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weights, topk):
+    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk, decode=True)
+
+
+def qwen3_next_moe_experts(x, gate_up_proj, down_proj, indices, weights, topk):
+    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk)
+
+
+def gpt_oss_moe_experts(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, topk):
+    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk, layout=LAYOUT_INTERLEAVED, act=ACT_GPTOSS,
+                       gate_up_bias=gate_up_bias, down_bias=down_bias)
+
+
+__all__ = [
+    "moe_experts", "route", "decode_supported",
+    "cohere2_moe_experts", "cohere2_moe_experts_decode",
+    "deepseek_ocr2_moe_experts", "deepseek_ocr2_moe_experts_decode",
+    "qwen3_next_moe_experts", "gpt_oss_moe_experts",
+    "LAYOUT_CONCAT", "LAYOUT_INTERLEAVED", "ACT_SILU", "ACT_GPTOSS",
+]

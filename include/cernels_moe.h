@@ -1,0 +1,141 @@
+/*
+ * cernels_moe.h — C ABI of the MI355X (gfx950) routed MoE-experts library, libcernels_moe.so.
+ *
+ * Plain pointers and sizes only; no torch types. Every entry point is asynchronous on the
+ * caller's HIP stream, performs no host synchronisation and allocates no device memory: the
+ * caller passes a workspace of at least the size the matching *_workspace_bytes() returns.
+ * All return a status (CERNELS_MOE_OK = 0); cernels_moe_status_string() names it.
+ *
+ * Tensor conventions (all row-major, contiguous, 16-byte aligned):
+ *   x              [T, H]   bf16         hidden states
+ *   indices        [T, K]   int32        top_k_index (expert id per token and slot)
+ *   weights        [T, K]   fp32         top_k_weights (routing weight per token and slot)
+ *   out            [T, H]   bf16         written in full
+ *   layout CONCAT:      gate_up_proj [E, 2F, H] (rows 0..F-1 gate, F..2F-1 up), down_proj [E, H, F]
+ *   layout INTERLEAVED: gate_up_proj [E, H, 2F] (even columns gate, odd up),   down_proj [E, F, H]
+ *   gate_up_bias   [E, 2F]  fp32 or NULL (same column order as the layout)
+ *   down_bias      [E, H]   fp32 or NULL
+ * Expert ids outside [0, E) contribute nothing (as the reference prefill op,
+ * src/kops/cohere2_moe_experts/csrc/cohere2_moe_experts.cu:35,49).
+ *
+ * Reference interface replaced: the torch ops registered in
+ *   src/kops/cohere2_moe_experts/torch-ext/torch_binding.cpp:6-13,
+ *   src/kops/deepseek_ocr2_moe_experts/torch-ext/torch_binding.cpp,
+ *   src/kops/qwen3_next_moe_experts/torch-ext/torch_binding.cpp,
+ *   src/kops/gpt_oss_moe_experts/torch-ext/torch_binding.cpp:7-10
+ * whose C++ signatures are in the matching torch-ext/torch_binding.h.
+ */
+#ifndef CERNELS_MOE_H
+#define CERNELS_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum cernels_moe_status {
+    CERNELS_MOE_OK = 0,
+    CERNELS_MOE_INVALID_ARGUMENT = 1,   /* null pointer, negative or zero dimension, bad enum */
+    CERNELS_MOE_UNSUPPORTED_SHAPE = 2,  /* shape outside what the kernels handle (see each entry) */
+    CERNELS_MOE_MISALIGNED = 3,         /* a tensor pointer is not 16-byte aligned */
+    CERNELS_MOE_WORKSPACE_TOO_SMALL = 4,
+    CERNELS_MOE_HIP_ERROR = 5           /* a kernel launch failed */
+};
+
+enum cernels_moe_layout { CERNELS_MOE_LAYOUT_CONCAT = 0, CERNELS_MOE_LAYOUT_INTERLEAVED = 1 };
+enum cernels_moe_act {
+    CERNELS_MOE_ACT_SILU = 0,   /* silu(gate) * up */
+    CERNELS_MOE_ACT_GPTOSS = 1  /* (clamp(up,-7,7) + 1) * g * sigmoid(1.702 g), g = min(gate, 7) */
+};
+
+const char* cernels_moe_version(void);
+const char* cernels_moe_status_string(int status);
+
+/* ---- routing (prefill): histogram -> offsets -> stable permutation -> M-tile list ---------------
+ * Replaces count_tokens_kernel + at::cumsum + build_perm_kernel
+ * (src/kops/cohere2_moe_experts/csrc/cohere2_moe_experts.cu:29-55, :262-284).
+ *   expert_offsets [E+1]: exclusive scan of per-expert pair counts; expert_offsets[E] = valid pairs.
+ *   sorted_pairs   [T*K]: pair ids p = t*K + k grouped by expert, within an expert by slot k then
+ *                         token t (the op_eager order); entries past expert_offsets[E] are unset.
+ *   tile_offsets   [E+1]: exclusive scan of ceil(count_e / tile_m).
+ *   tile_expert    [cernels_moe_route_tile_capacity()]: expert of each M-tile.
+ *   meta           [2]  : meta[0] = number of M-tiles, meta[1] = valid pairs.
+ * Limits: 1 <= E <= 1024, T*K < 2^31, tile_m >= 1. */
+size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t tile_m);
+int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, int32_t tile_m,
+                      int32_t* expert_offsets, int32_t* sorted_pairs, int32_t* tile_offsets,
+                      int32_t* tile_expert, int32_t* meta, hipStream_t stream);
+
+/* ---- prefill: grouped GEMM experts ------------------------------------------------------------
+ * route -> gate_up GEMM (+bias, SwiGLU in the epilogue) -> down GEMM (+bias, x routing weight in
+ * the epilogue) -> deterministic top-k combine. Any T >= 0 (T = 0 is a no-op).
+ * Limits: H % 64 == 0, F % 64 == 0, E <= 1024. */
+size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K);
+int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                        const void* down_proj, const float* down_bias, const int32_t* indices,
+                        const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                        int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/* ---- decode: fused gather-GEMV over the distinct selected experts -------------------------------
+ * Two launches, no atomics on the output, no host sync. Layout CONCAT only.
+ * Limits: T <= cernels_moe_decode_max_tokens(), T*K <= cernels_moe_decode_max_pairs(),
+ * H % 8 == 0, F % 8 == 0, H <= 4096, F <= 4096. */
+int32_t cernels_moe_decode_max_tokens(void);
+int32_t cernels_moe_decode_max_pairs(void);
+size_t cernels_moe_experts_decode_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K);
+int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                               const void* down_proj, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t layout, int32_t act, void* out, void* workspace,
+                               size_t workspace_bytes, hipStream_t stream);
+
+/* ---- the reference's per-model ops, same argument order as their torch schemas ----------------
+ * cohere2_moe_experts(Tensor x, Tensor gate_up_proj, Tensor down_proj, Tensor indices,
+ *                     Tensor weights, int topk) -> Tensor
+ *   (src/kops/cohere2_moe_experts/torch-ext/torch_binding.cpp:7-9; .cu:238-361)
+ * cohere2_moe_experts_decode(...)            (torch_binding.cpp:10-12; .cu:199-236)
+ * deepseek_ocr2_moe_experts(...) / _decode   (src/kops/deepseek_ocr2_moe_experts/csrc/
+ *                                             deepseek_ocr2_moe_experts.cu:240-363 / :201-238)
+ * qwen3_next_moe_experts(...)                (src/kops/qwen3_next_moe_experts/csrc/
+ *                                             qwen3_next_moe_experts.cu:97-220)
+ * Concat layout, SiLU; T, H, F, E come from the tensor shapes on the torch side. */
+int cernels_cohere2_moe_experts(const void* x, const void* gate_up_proj, const void* down_proj,
+                                const int32_t* indices, const float* weights, int32_t T, int32_t H,
+                                int32_t F, int32_t E, int32_t topk, void* out, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
+int cernels_cohere2_moe_experts_decode(const void* x, const void* gate_up_proj, const void* down_proj,
+                                       const int32_t* indices, const float* weights, int32_t T,
+                                       int32_t H, int32_t F, int32_t E, int32_t topk, void* out,
+                                       void* workspace, size_t workspace_bytes, hipStream_t stream);
+int cernels_deepseek_ocr2_moe_experts(const void* x, const void* gate_up_proj, const void* down_proj,
+                                      const int32_t* indices, const float* weights, int32_t T,
+                                      int32_t H, int32_t F, int32_t E, int32_t topk, void* out,
+                                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+int cernels_deepseek_ocr2_moe_experts_decode(const void* x, const void* gate_up_proj,
+                                             const void* down_proj, const int32_t* indices,
+                                             const float* weights, int32_t T, int32_t H, int32_t F,
+                                             int32_t E, int32_t topk, void* out, void* workspace,
+                                             size_t workspace_bytes, hipStream_t stream);
+int cernels_qwen3_next_moe_experts(const void* x, const void* gate_up_proj, const void* down_proj,
+                                   const int32_t* indices, const float* weights, int32_t T, int32_t H,
+                                   int32_t F, int32_t E, int32_t topk, void* out, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream);
+/* gpt_oss_moe_experts(Tensor x, Tensor gate_up_proj, Tensor gate_up_bias, Tensor down_proj,
+ *                     Tensor down_bias, Tensor indices, Tensor weights, int topk) -> Tensor
+ *   (src/kops/gpt_oss_moe_experts/torch-ext/torch_binding.cpp:7-10; .cu:119-245)
+ * Interleaved layout, fp32 biases, clamped SwiGLU. */
+int cernels_gpt_oss_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                                const void* down_proj, const float* down_bias, const int32_t* indices,
+                                const float* weights, int32_t T, int32_t H, int32_t F, int32_t E,
+                                int32_t topk, void* out, void* workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CERNELS_MOE_H */

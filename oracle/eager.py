@@ -1,0 +1,168 @@
+"""CPU oracle for the routed MoE-experts path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may import this
+module; the product path (cernels_amd) never does.
+
+What it restates (third-party algorithm: transformers 5.15.0, the reference pins >=5.10.2 in
+pyproject.toml:15; the reference's configs call these modules as their op_eager baseline,
+src/configs/registry/cohere2_moe_experts.py:81-85, gpt_oss_moe_experts.py:62-67):
+
+* ``experts_eager``  — ``Cohere2MoeExperts.forward`` (models/cohere2_moe/modeling_cohere2_moe.py
+  :114-138; DeepseekOcr2TextExperts :1150-1174 and Qwen3NextExperts :730-754 are the same code)
+  and ``GptOssExperts.forward`` (models/gpt_oss/modeling_gpt_oss.py:90-114, ``_apply_gate``
+  :82-88): the same torch ops in the same order, bf16 throughout, ``index_add_`` in bf16 over
+  the hit experts in ascending order. Expert ids outside [0, E) are skipped, as the reference's
+  CUDA op does (src/kops/cohere2_moe_experts/csrc/cohere2_moe_experts.cu:35,49).
+* ``experts_fp64``   — the same mathematics with every operand upcast to float64 and no
+  intermediate rounding: the exact value of the op on the given bf16 inputs.
+* ``route_reference`` — offsets / permutation / tile list in op_eager order, by the closed form
+  ``argsort(index.T.flatten(), stable)`` and ``bincount`` (numpy).
+
+Parity pins (tests/test_oracle.py): ``experts_eager`` equals transformers' own forward bit for
+bit on the committed golden fixtures (tests/golden/, written by tests/golden/make_golden.py);
+``experts_fp64`` equals a per-(token, slot) brute-force loop and the closed-form special cases
+(E=1,k=1 dense MLP; zero weights; gpt-oss clamps; relabelling invariance; linearity);
+``route_reference`` equals the golden ``torch.where`` order and the C restatement oracle/route.c.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+LAYOUT_CONCAT = "concat"
+LAYOUT_INTERLEAVED = "interleaved"
+ACT_SILU = "silu"
+ACT_GPTOSS = "gptoss"
+GPTOSS_ALPHA = 1.702
+GPTOSS_LIMIT = 7.0
+
+
+def gptoss_gate(gate_up: torch.Tensor) -> torch.Tensor:
+    """GptOssExperts._apply_gate (modeling_gpt_oss.py:82-88)."""
+    gate, up = gate_up[..., ::2], gate_up[..., 1::2]
+    gate = gate.clamp(min=None, max=GPTOSS_LIMIT)
+    up = up.clamp(min=-GPTOSS_LIMIT, max=GPTOSS_LIMIT)
+    glu = gate * torch.sigmoid(gate * GPTOSS_ALPHA)
+    return (up + 1) * glu
+
+
+def _valid_mask_index(top_k_index: torch.Tensor, E: int) -> torch.Tensor:
+    """Map out-of-range ids to E (a class the loop skips, like transformers' `== num_experts`)."""
+    idx = top_k_index.to(torch.int64)
+    return torch.where((idx >= 0) & (idx < E), idx, torch.full_like(idx, E))
+
+
+def experts_eager(x, top_k_index, top_k_weights, gate_up_proj, down_proj, gate_up_bias=None, down_bias=None,
+                  layout=LAYOUT_CONCAT, act=ACT_SILU):
+    """op_eager restatement on whatever device/dtype the inputs have (bf16 on CPU for parity)."""
+    E = gate_up_proj.shape[0]
+    final = torch.zeros_like(x)
+    with torch.no_grad():
+        idx = _valid_mask_index(top_k_index, E)
+        expert_mask = F.one_hot(idx, num_classes=E + 1).permute(2, 1, 0)
+        expert_hit = torch.greater(expert_mask.sum(dim=(-1, -2)), 0).nonzero()
+        for expert_idx in expert_hit:
+            expert_idx = expert_idx[0]
+            if expert_idx == E:
+                continue
+            top_k_pos, token_idx = torch.where(expert_mask[expert_idx])
+            cur = x[token_idx]
+            if layout == LAYOUT_CONCAT:
+                gu = F.linear(cur, gate_up_proj[expert_idx])
+                if gate_up_bias is not None:
+                    gu = gu + gate_up_bias[expert_idx]
+                if act == ACT_SILU:
+                    gate, up = gu.chunk(2, dim=-1)
+                    h = F.silu(gate) * up
+                else:  # gpt-oss gate on the concat layout: gate/up halves
+                    gate, up = gu.chunk(2, dim=-1)
+                    h = gptoss_gate(torch.stack((gate, up), dim=-1).flatten(-2))
+                h = F.linear(h, down_proj[expert_idx])
+            else:
+                gu = cur @ gate_up_proj[expert_idx]
+                if gate_up_bias is not None:
+                    gu = gu + gate_up_bias[expert_idx]
+                if act == ACT_GPTOSS:
+                    h = gptoss_gate(gu)
+                else:
+                    gate, up = gu[..., ::2], gu[..., 1::2]
+                    h = F.silu(gate) * up
+                h = h @ down_proj[expert_idx]
+            if down_bias is not None:
+                h = h + down_bias[expert_idx]
+            h = h * top_k_weights[token_idx, top_k_pos, None]
+            final.index_add_(0, token_idx, h.to(final.dtype))
+    return final
+
+
+def experts_fp64(x, top_k_index, top_k_weights, gate_up_proj, down_proj, gate_up_bias=None, down_bias=None,
+                 layout=LAYOUT_CONCAT, act=ACT_SILU):
+    """Exact value on the given inputs: float64 everywhere, no intermediate rounding. Returns fp64."""
+    d = torch.float64
+    x, w = x.to(d), top_k_weights.to(d)
+    E = gate_up_proj.shape[0]
+    out = torch.zeros(x.shape, dtype=d)
+    idx = _valid_mask_index(top_k_index, E)
+    for e in torch.unique(idx).tolist():
+        if e == E:
+            continue
+        tpos, kpos = torch.where(idx == e)
+        cur = x[tpos]
+        W1 = gate_up_proj[e].to(d)
+        gu = cur @ (W1.T if layout == LAYOUT_CONCAT else W1)
+        if gate_up_bias is not None:
+            gu = gu + gate_up_bias[e].to(d)
+        if layout == LAYOUT_CONCAT:
+            gate, up = gu.chunk(2, dim=-1)
+        else:
+            gate, up = gu[..., ::2], gu[..., 1::2]
+        if act == ACT_SILU:
+            h = F.silu(gate) * up
+        else:
+            h = gptoss_gate(torch.stack((gate, up), dim=-1).flatten(-2))
+        W2 = down_proj[e].to(d)
+        y = h @ (W2.T if layout == LAYOUT_CONCAT else W2)
+        if down_bias is not None:
+            y = y + down_bias[e].to(d)
+        out.index_add_(0, tpos, y * w[tpos, kpos, None])
+    return out
+
+
+def route_reference(top_k_index, num_experts: int, tile_m: int = 128) -> dict[str, np.ndarray]:
+    """Closed-form routing in op_eager order.
+
+    offsets = [0] + cumsum(bincount(valid ids)); sorted_pairs = pair ids p = t*K + k ordered by
+    (expert, k, t) = stable argsort of index.T.flatten() (modeling_cohere2_moe.py:122-130 reads
+    the [K, T] one-hot slice row-major); tiles = ceil(count_e / tile_m) per expert.
+    """
+    idx = np.asarray(top_k_index, dtype=np.int64)
+    T, K = idx.shape
+    flat_kt = idx.T.reshape(-1)  # slot-major: q = k*T + t
+    valid = (flat_kt >= 0) & (flat_kt < num_experts)
+    q = np.nonzero(valid)[0]
+    order = q[np.argsort(flat_kt[q], kind="stable")]
+    k_of, t_of = order // T, order % T
+    sorted_pairs = (t_of * K + k_of).astype(np.int32)
+    counts = np.bincount(flat_kt[valid], minlength=num_experts).astype(np.int64)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    ntiles = -(-counts // tile_m)
+    tile_offsets = np.concatenate([[0], np.cumsum(ntiles)]).astype(np.int32)
+    tile_expert = np.repeat(np.arange(num_experts, dtype=np.int32), ntiles)
+    return {
+        "offsets": offsets,
+        "sorted_pairs": sorted_pairs,
+        "tile_offsets": tile_offsets,
+        "tile_expert": tile_expert,
+        "num_tiles": int(tile_offsets[-1]),
+        "num_valid": int(offsets[-1]),
+    }
+
+
+def error_stats(out: torch.Tensor, ref: torch.Tensor) -> dict[str, float]:
+    """max |out - ref| and RMS(ref) (both fp64); the bar is max_abs <= 2e-2 * rms."""
+    o, r = out.double().cpu(), ref.double().cpu()
+    rms = float(r.pow(2).mean().sqrt()) if r.numel() else 0.0
+    mx = float((o - r).abs().max()) if r.numel() else 0.0
+    return {"max_abs": mx, "rms_ref": rms, "ratio": mx / rms if rms > 0 else (0.0 if mx == 0 else float("inf"))}
