@@ -15,14 +15,15 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
                           int32_t* sorted_pairs, int32_t* tile_expert, int max_tiles, uint16_t* glu, float* Y,
-                          hipStream_t s);
+                          hipStream_t s, hipEvent_t* ev);
 bool decode_shape_supported(int H, int F);
 int decode_max_pairs();
 int decode_max_tokens();
 int decode_h_block();
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
                          const int32_t* idx, const float* route_w, float* glu, float* Y, int32_t* tickets,
-                         uint16_t* out, int T, int H, int F, int E, int K, int act, hipStream_t s);
+                         uint16_t* out, int T, int H, int F, int E, int K, int act, hipStream_t s,
+                         hipEvent_t* ev);
 }  // namespace cmoe
 
 namespace {
@@ -132,10 +133,11 @@ size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int3
     return prefill_ws(T, H, F, E, K).total;
 }
 
-int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias, const void* down_proj,
-                        const float* down_bias, const int32_t* indices, const float* weights, int32_t T, int32_t H,
-                        int32_t F, int32_t E, int32_t K, int32_t layout, int32_t act, void* out, void* workspace,
-                        size_t workspace_bytes, hipStream_t stream) {
+int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                               const void* down_proj, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream, hipEvent_t* stage_events) {
     int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
     if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
@@ -147,7 +149,15 @@ int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* ga
         reinterpret_cast<int32_t*>(base + w.offsets), reinterpret_cast<int32_t*>(base + w.tile_offsets),
         reinterpret_cast<int32_t*>(base + w.meta), reinterpret_cast<int32_t*>(base + w.sorted_pairs),
         reinterpret_cast<int32_t*>(base + w.tile_expert), w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
-        reinterpret_cast<float*>(base + w.Y), stream));
+        reinterpret_cast<float*>(base + w.Y), stream, stage_events));
+}
+
+int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias, const void* down_proj,
+                        const float* down_bias, const int32_t* indices, const float* weights, int32_t T, int32_t H,
+                        int32_t F, int32_t E, int32_t K, int32_t layout, int32_t act, void* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+    return cernels_moe_experts_staged(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, T, H, F,
+                                      E, K, layout, act, out, workspace, workspace_bytes, stream, nullptr);
 }
 
 int32_t cernels_moe_decode_max_tokens(void) { return cmoe::decode_max_tokens(); }
@@ -158,11 +168,11 @@ size_t cernels_moe_experts_decode_workspace_bytes(int32_t T, int32_t H, int32_t 
     return decode_ws(T, H, F, K).total;
 }
 
-int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const float* gate_up_bias,
-                               const void* down_proj, const float* down_bias, const int32_t* indices,
-                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
-                               int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
-                               hipStream_t stream) {
+int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                                      const void* down_proj, const float* down_bias, const int32_t* indices,
+                                      const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                                      int32_t layout, int32_t act, void* out, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events) {
     int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
     if (layout != CERNELS_MOE_LAYOUT_CONCAT) return CERNELS_MOE_UNSUPPORTED_SHAPE;
@@ -175,7 +185,17 @@ int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const fl
         static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(gate_up_proj), gate_up_bias,
         static_cast<const uint16_t*>(down_proj), down_bias, indices, weights, reinterpret_cast<float*>(base + w.glu),
         reinterpret_cast<float*>(base + w.Y), reinterpret_cast<int32_t*>(base + w.tickets),
-        static_cast<uint16_t*>(out), T, H, F, E, K, act, stream));
+        static_cast<uint16_t*>(out), T, H, F, E, K, act, stream, stage_events));
+}
+
+int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                               const void* down_proj, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+    return cernels_moe_experts_decode_staged(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights,
+                                             T, H, F, E, K, layout, act, out, workspace, workspace_bytes, stream,
+                                             nullptr);
 }
 
 // ---- the reference's per-model ops ----------------------------------------------------------------

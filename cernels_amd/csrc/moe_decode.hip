@@ -285,8 +285,12 @@ bool decode_shape_supported(int H, int F) { return pick_maxc(H) > 0 && pick_maxc
 
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
                          const int32_t* idx, const float* route_w, float* glu, float* Y, int32_t* tickets,
-                         uint16_t* out, int T, int H, int F, int E, int K, int act, hipStream_t s) {
+                         uint16_t* out, int T, int H, int F, int E, int K, int act, hipStream_t s,
+                         hipEvent_t* ev) {
+    // ev (optional): 3 events recorded before gate_up, after gate_up, after down.
+    auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     const int cg = pick_maxc(H), cd = pick_maxc(F);
+    mark(0);
     const int n_tickets = ceil_div(H, kDecHBlock);
     const bool bias = b1 != nullptr;
     if (act == kActSilu) {
@@ -296,8 +300,11 @@ hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1,
     }
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return st;
+    mark(1);
     if (b2 != nullptr) { CMOE_DEC_DN_ALL(true) } else { CMOE_DEC_DN_ALL(false) }
-    return hipGetLastError();
+    st = hipGetLastError();
+    mark(2);
+    return st;
 }
 
 }  // namespace cmoe

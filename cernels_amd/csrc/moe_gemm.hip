@@ -359,9 +359,14 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
                           int32_t* sorted_pairs, int32_t* tile_expert, int max_tiles, uint16_t* glu, float* Y,
-                          hipStream_t s) {
+                          hipStream_t s, hipEvent_t* ev) {
+    // ev (optional): 5 events recorded before route, after route, after gate_up, after down,
+    // after combine — for per-stage timing on the caller's stream.
+    auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
+    mark(0);
     hipError_t st = launch_route(idx, T, K, E, kBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, s);
     if (st != hipSuccess) return st;
+    mark(1);
     const bool concat = layout == kLayoutConcat;
     GemmParams g1{};
     g1.A = static_cast<const uint16_t*>(x);
@@ -383,6 +388,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g1.ldb = concat ? H : 2 * F;
     st = launch_gateup(g1, layout, act, b1 != nullptr, max_tiles, s);
     if (st != hipSuccess) return st;
+    mark(2);
     GemmParams g2 = g1;
     g2.A = glu;
     g2.B = static_cast<const uint16_t*>(w2);
@@ -395,7 +401,10 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g2.ldb = concat ? F : H;
     st = launch_down(g2, layout, b2 != nullptr, max_tiles, s);
     if (st != hipSuccess) return st;
-    return launch_combine(Y, idx, static_cast<uint16_t*>(out), T, K, E, H, s);
+    mark(3);
+    st = launch_combine(Y, idx, static_cast<uint16_t*>(out), T, K, E, H, s);
+    mark(4);
+    return st;
 }
 
 }  // namespace cmoe

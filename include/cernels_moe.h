@@ -80,6 +80,15 @@ int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* ga
                         int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
+/* Same as cernels_moe_experts, and, when stage_events is not NULL, records 5 caller-created
+ * events on `stream`: before routing, after routing, after the gate_up GEMM, after the down GEMM
+ * and after the combine (per-stage timing; no work is skipped). No counterpart in the reference. */
+int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                               const void* down_proj, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream, hipEvent_t* stage_events);
+
 /* ---- decode: fused gather-GEMV over the distinct selected experts -------------------------------
  * Two launches, no atomics on the output, no host sync. Layout CONCAT only.
  * Limits: T <= cernels_moe_decode_max_tokens(), T*K <= cernels_moe_decode_max_pairs(),
@@ -92,6 +101,13 @@ int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const fl
                                const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
                                int32_t layout, int32_t act, void* out, void* workspace,
                                size_t workspace_bytes, hipStream_t stream);
+
+/* Decode with 3 stage events (before gate_up, after gate_up, after down) when not NULL. */
+int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                                      const void* down_proj, const float* down_bias, const int32_t* indices,
+                                      const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                                      int32_t layout, int32_t act, void* out, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events);
 
 /* ---- the reference's per-model ops, same argument order as their torch schemas ----------------
  * cohere2_moe_experts(Tensor x, Tensor gate_up_proj, Tensor down_proj, Tensor indices,
