@@ -83,9 +83,9 @@ def stage_model(shape, U, P, stage):
     if stage == "combine":
         return float(P * H), P * H * 4 + T * H * 2 + P * 4
     if stage == "decode_gate_up":
-        return 2.0 * P * H * 2 * F, U * 2 * F * H * 2 + T * H * 2 + P * F * 4
+        return 2.0 * P * H * 2 * F, U * 2 * F * H * 2 + T * H * 2 + P * F * 2
     if stage == "decode_down":
-        return 2.0 * P * F * H, U * H * F * 2 + P * F * 4 + P * H * 4 + T * H * 2
+        return 2.0 * P * F * H, U * H * F * 2 + P * F * 2 + T * H * 2
     raise KeyError(stage)
 
 

@@ -19,11 +19,9 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
 bool decode_shape_supported(int H, int F);
 int decode_max_pairs();
 int decode_max_tokens();
-int decode_h_block();
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
-                         const int32_t* idx, const float* route_w, float* glu, float* Y, int32_t* tickets,
-                         uint16_t* out, int T, int H, int F, int E, int K, int act, hipStream_t s,
-                         hipEvent_t* ev);
+                         const int32_t* idx, const float* route_w, uint16_t* glu, uint16_t* out, int T, int H, int F,
+                         int E, int K, int act, hipStream_t s, hipEvent_t* ev);
 }  // namespace cmoe
 
 namespace {
@@ -57,16 +55,15 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
 }
 
 struct DecodeWs {
-    size_t glu, Y, tickets, total;
+    size_t glu, total;
 };
 
 DecodeWs decode_ws(int T, int H, int F, int K) {
+    (void)H;
     DecodeWs w{};
     const long long P = (long long)T * K;
     size_t o = 0;
-    w.glu = o;     o = align_up(o + sizeof(float) * P * F);
-    w.Y = o;       o = align_up(o + sizeof(float) * P * H);
-    w.tickets = o; o = align_up(o + sizeof(int32_t) * ((H + cmoe::decode_h_block() - 1) / cmoe::decode_h_block()));
+    w.glu = o; o = align_up(o + sizeof(uint16_t) * P * F);
     w.total = o;
     return w;
 }
@@ -183,9 +180,9 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
     char* base = static_cast<char*>(workspace);
     return hip_status(cmoe::launch_decode(
         static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(gate_up_proj), gate_up_bias,
-        static_cast<const uint16_t*>(down_proj), down_bias, indices, weights, reinterpret_cast<float*>(base + w.glu),
-        reinterpret_cast<float*>(base + w.Y), reinterpret_cast<int32_t*>(base + w.tickets),
-        static_cast<uint16_t*>(out), T, H, F, E, K, act, stream, stage_events));
+        static_cast<const uint16_t*>(down_proj), down_bias, indices, weights,
+        reinterpret_cast<uint16_t*>(base + w.glu), static_cast<uint16_t*>(out), T, H, F, E, K, act, stream,
+        stage_events));
 }
 
 int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const float* gate_up_bias,

@@ -22,6 +22,8 @@
 // register double buffer; 16-byte chunks are XOR-swizzled by (row & 7) against bank conflicts.
 // GEMM1's B tile holds 64 gate rows then the 64 matching up rows, so one lane owns the gate and
 // the up value of the same output column and the SwiGLU happens in registers.
+#include <stdlib.h>
+
 #include "moe_common.h"
 
 namespace cmoe {
@@ -73,6 +75,191 @@ __device__ __forceinline__ void transpose_4x8(const u32x4 (&v)[4], u32x2 (&o)[8]
             o[j][0] = (a0 & 0xffffu) | (a1 << 16);
             o[j][1] = (a2 & 0xffffu) | (a3 << 16);
         }
+    }
+}
+
+// ---- direct global -> LDS copies (gfx950 global_load_lds_dwordx4) ---------------------------------
+// One instruction moves 16 bytes per lane into LDS at M0 + 16*lane (1 KB per wave). The load is
+// issued from inline assembly so the compiler does not wait for every outstanding copy at each
+// barrier; completion is awaited explicitly with s_waitcnt vmcnt(N) before the barrier that
+// publishes a stage.
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const unsigned char*)(p));
+}
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Multi-stage grouped GEMM for K-contiguous weights (concat layout): A rows (gathered tokens or
+// glu rows) and B rows (weight rows) stream HBM -> LDS directly, STAGES deep, so up to STAGES-1
+// k-steps of loads are in flight while the MFMAs consume the oldest stage. One workgroup of
+// 256 threads per CU (STAGES x 32 KB of LDS).
+template <int MODE, int ACT, bool HAS_BIAS, int STAGES>
+__global__ __launch_bounds__(kGemmThreads, STAGES <= 2 ? 2 : 1) void moe_gemm_dma_kernel(GemmParams prm) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int kStageBytes = 2 * kTileBytes;
+    constexpr int kPer = kBM / 8 / 4;  // 1 KB copies per wave per operand per stage (= 4)
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int wm = wave & 1, wn = wave >> 1;
+    const uint32_t lds0 = lds_u32(smem);
+
+    const int tiles = prm.meta[0];
+    const int total = tiles * prm.n_tiles;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
+    const int per = ceil_div(total, 8);
+    const int it_end = min(total, (xcd + 1) * per);
+
+    // lane -> (row within an 8-row group, swizzled 16-byte chunk) of its copies
+    const int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
+
+    for (int it = xcd * per + slot; it < it_end; it += slots) {
+        const int e = prm.tile_expert[it / prm.n_tiles];
+        const int t0 = prm.tile_offsets[e], nt_e = prm.tile_offsets[e + 1] - t0;
+        const int local = it - t0 * prm.n_tiles;
+        const int n_idx = local / nt_e, m_idx = local - n_idx * nt_e;
+        const int seg0 = prm.offsets[e], seg_n = prm.offsets[e + 1] - seg0;
+        const int row_begin = seg0 + m_idx * kBM;
+        const int rows = min(kBM, seg_n - m_idx * kBM);
+        const int n0 = n_idx * (MODE == kModeGateUp ? kBN / 2 : kBN);
+        const uint16_t* Be = prm.B + (long long)e * prm.expert_stride;
+        const int Kd = prm.Kdim;
+
+        const uint16_t* a_src[kPer];
+        const uint16_t* b_src[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int r = 8 * (i * 4 + wave) + lrow;  // tile row of this lane's copy
+            const int ra = min(r, rows - 1);
+            long long src_row;
+            if constexpr (MODE == kModeGateUp) src_row = prm.sorted_pairs[row_begin + ra] / prm.topk;
+            else src_row = row_begin + ra;
+            a_src[i] = prm.A + src_row * Kd + lchunk * 8;
+            int wrow;
+            if constexpr (MODE == kModeGateUp) {
+                const int c = min(n0 + (r & 63), prm.F - 1);
+                wrow = r < 64 ? c : prm.F + c;
+            } else {
+                wrow = min(n0 + r, prm.N - 1);
+            }
+            b_src[i] = Be + (long long)wrow * prm.ldb + lchunk * 8;
+        }
+        auto issue = [&](int kt, int stage) {
+            const uint32_t sa = lds0 + stage * kStageBytes + wave * 1024;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) dma16(a_src[i] + kt * kBK, sa + i * 4096);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) dma16(b_src[i] + kt * kBK, sa + kTileBytes + i * 4096);
+        };
+
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+        int brow[2];
+        if constexpr (MODE == kModeGateUp) {
+            brow[0] = wn * 32;
+            brow[1] = 64 + wn * 32;
+        } else {
+            brow[0] = wn * 64;
+            brow[1] = wn * 64 + 32;
+        }
+        const int arow0 = wm * 64 + (lane & 31);
+        const int khalf = lane >> 5;
+        const int nk = Kd / kBK;
+
+        wait_vmcnt<0>();  // the index loads above must not be counted against the copies below
+#pragma unroll
+        for (int s = 0; s < STAGES - 1; ++s)
+            if (s < nk) issue(s, s);
+        for (int kt = 0; kt < nk; ++kt) {
+            // copies of stages kt+1 .. min(kt+STAGES-2, nk-1) may stay in flight
+            const int younger = min(STAGES - 2, nk - 1 - kt);
+            if (younger >= STAGES - 2) wait_vmcnt<2 * kPer * (STAGES - 2)>();
+            else if (STAGES >= 4 && younger == 2) wait_vmcnt<2 * kPer * 2>();
+            else if (STAGES >= 3 && younger == 1) wait_vmcnt<2 * kPer>();
+            else wait_vmcnt<0>();
+            __syncthreads();
+            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+            const unsigned char* sA = smem + (kt % STAGES) * kStageBytes;
+            const unsigned char* sB = sA + kTileBytes;
+            // all 16 fragments of this k-step first, so the MFMAs of sub-step ks overlap the LDS
+            // reads of the later sub-steps
+            bf16x8 af[kBK / 16][2], bfr[kBK / 16][2];
+#pragma unroll
+            for (int ks = 0; ks < kBK / 16; ++ks) {
+                const int chunk = ks * 2 + khalf;
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                    af[ks][mb] = *reinterpret_cast<const bf16x8*>(sA + lds_off(arow0 + mb * 32, chunk));
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+                    bfr[ks][nb] = *reinterpret_cast<const bf16x8*>(sB + lds_off(brow[nb] + (lane & 31), chunk));
+            }
+#pragma unroll
+            for (int ks = 0; ks < kBK / 16; ++ks)
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb)
+                        acc[mb][nb] =
+                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][mb], bfr[ks][nb], acc[mb][nb], 0, 0, 0);
+        }
+
+        if constexpr (MODE == kModeGateUp) {
+            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+            const int n = n0 + wn * 32 + (lane & 31);
+            if (n < prm.N) {
+                float bg = 0.f, bu = 0.f;
+                if constexpr (HAS_BIAS) {
+                    const float* be = prm.bias + (long long)e * 2 * prm.F;
+                    bg = be[n];
+                    bu = be[prm.F + n];
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row < rows) {
+                            const float v = swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu);
+                            glu[(long long)(row_begin + row) * prm.F + n] = f32_to_bf16_bits(v);
+                        }
+                    }
+            }
+        } else {
+            float* Y = reinterpret_cast<float*>(prm.out);
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < rows) {
+                        const int p = prm.sorted_pairs[row_begin + row];
+                        const float w = prm.route_w[p];
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb) {
+                            const int n = n0 + brow[nb] + (lane & 31);
+                            if (n < prm.N) {
+                                float v = acc[mb][nb][r];
+                                if constexpr (HAS_BIAS) v += prm.bias[(long long)e * prm.N + n];
+                                Y[(long long)p * prm.N + n] = v * w;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();  // every wave is done with the LDS stages before the next item's copies
     }
 }
 
@@ -309,14 +496,53 @@ static int cu_count() {
 
 int gemm_tile_m() { return kBM; }
 
+// LDS pipeline depth of the concat-layout GEMM: 2 stages (64 KB, two workgroups per CU) by
+// default — measured faster on MI355X than 3 or 4 stages with one workgroup per CU, because the
+// second workgroup covers the first one's item prologue and epilogue. CERNELS_GEMM_STAGES=3|4
+// selects the deeper single-workgroup pipelines.
+static int gemm_stages() {
+    static int stages = 0;
+    if (stages == 0) {
+        const char* v = getenv("CERNELS_GEMM_STAGES");
+        const int s = v ? atoi(v) : 2;
+        stages = (s == 3 || s == 4) ? s : 2;
+    }
+    return stages;
+}
+
+template <int MODE, int ACT, bool HAS_BIAS, int STAGES>
+static hipError_t launch_dma_t(const GemmParams& prm, int upper, hipStream_t stream) {
+    static bool attr = false;
+    const size_t lds = (size_t)STAGES * 2 * kTileBytes;
+    if (!attr) {
+        hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_dma_kernel<MODE, ACT, HAS_BIAS, STAGES>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (st != hipSuccess) return st;
+        attr = true;
+    }
+    int grid = min(upper, cu_count() * (STAGES <= 2 ? 2 : 1));
+    grid = ceil_div(max(grid, 1), 8) * 8;
+    hipLaunchKernelGGL((moe_gemm_dma_kernel<MODE, ACT, HAS_BIAS, STAGES>), dim3(grid), dim3(kGemmThreads), lds, stream,
+                       prm);
+    return hipGetLastError();
+}
+
 template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
 static hipError_t launch_gemm_t(const GemmParams& prm, int max_tiles, hipStream_t stream) {
     const int upper = max_tiles * prm.n_tiles;
-    int grid = min(upper, cu_count() * 2);
-    grid = ceil_div(max(grid, 1), 8) * 8;
-    const size_t lds = 4 * (size_t)kTileBytes;
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>), dim3(grid), dim3(kGemmThreads), lds, stream,
-                       prm);
+    if constexpr (LAYOUT == kLayoutConcat) {
+        switch (gemm_stages()) {
+            case 2: return launch_dma_t<MODE, ACT, HAS_BIAS, 2>(prm, upper, stream);
+            case 3: return launch_dma_t<MODE, ACT, HAS_BIAS, 3>(prm, upper, stream);
+            default: return launch_dma_t<MODE, ACT, HAS_BIAS, 4>(prm, upper, stream);
+        }
+    } else {
+        int grid = min(upper, cu_count() * 2);
+        grid = ceil_div(max(grid, 1), 8) * 8;
+        const size_t lds = 4 * (size_t)kTileBytes;
+        hipLaunchKernelGGL((moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>), dim3(grid), dim3(kGemmThreads), lds,
+                           stream, prm);
+    }
     return hipGetLastError();
 }
 

@@ -46,26 +46,50 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot, int* t
     return before + x - v;
 }
 
+constexpr uint16_t kNoExpert = 0xffff;
+
+// STAGED: every expert id is first copied into LDS as uint16 in slot-major order (coalesced,
+// many loads in flight); the histogram and scatter phases then never touch global memory.
+template <bool STAGED>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     const int32_t* __restrict__ idx, int T, int K, int E, int BM, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ meta) {
-    extern __shared__ int32_t hist[];  // [kRouteWaves][E]
+    extern __shared__ int32_t hist[];  // [kRouteWaves][E], then (STAGED) uint16 ids [P]
     __shared__ int wave_tot[kRouteWaves];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
     const int P = T * K;
+    uint16_t* eid = reinterpret_cast<uint16_t*>(hist + kRouteWaves * E);
 
     for (int i = tid; i < kRouteWaves * E; i += kRouteThreads) hist[i] = 0;
+    if constexpr (STAGED) {
+#pragma unroll 8
+        for (int i = tid; i < P; i += kRouteThreads) {
+            const int v = idx[i];
+            const int t = i / K, k = i - t * K;
+            eid[k * T + t] = ((unsigned)v < (unsigned)E) ? (uint16_t)v : kNoExpert;
+        }
+    }
     __syncthreads();
+    // expert id of slot-major pair q (-1 if out of range)
+    auto expert_at = [&](int q) -> int {
+        if constexpr (STAGED) {
+            const uint16_t v = eid[q];
+            return v == kNoExpert ? -1 : (int)v;
+        } else {
+            const int k = q / T, t = q - k * T;
+            const int v = idx[t * K + k];
+            return ((unsigned)v < (unsigned)E) ? v : -1;
+        }
+    };
 
     const int seg = ceil_div(ceil_div(P, kRouteWaves), kWave) * kWave;
     const int q0 = min(P, w * seg), q1 = min(P, q0 + seg);
 
     // 1. per-wave histogram (order-free, so LDS atomics are fine here)
     for (int q = q0 + lane; q < q1; q += kWave) {
-        const int k = q / T, t = q - k * T;
-        const int e = idx[t * K + k];
-        if ((unsigned)e < (unsigned)E) atomicAdd(&hist[w * E + e], 1);
+        const int e = expert_at(q);
+        if (e >= 0) atomicAdd(&hist[w * E + e], 1);
     }
     __syncthreads();
 
@@ -107,8 +131,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         if (q < q1) {
             const int k = q / T, t = q - k * T;
             p = t * K + k;
-            const int v = idx[p];
-            if ((unsigned)v < (unsigned)E) ex = v;
+            ex = expert_at(q);
         }
         const bool valid = ex >= 0;
         uint64_t m = __ballot(valid);
@@ -127,20 +150,46 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     }
 }
 
-size_t route_lds_bytes(int E) { return (size_t)kRouteWaves * E * sizeof(int32_t); }
+static size_t route_hist_bytes(int E) { return (size_t)kRouteWaves * E * sizeof(int32_t); }
+
+static int max_lds_per_block() {
+    static int v = 0;
+    if (v == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess && n > 0)
+            v = n;
+        else
+            v = 64 * 1024;
+    }
+    return v;
+}
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, hipStream_t stream) {
-    const size_t lds = route_lds_bytes(E);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t st = hipFuncSetAttribute((const void*)moe_route_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            (int)route_lds_bytes(kRouteThreads));
-        if (st != hipSuccess) return st;
-        attr_set = true;
+    const int cap = max_lds_per_block() - 1024;  // room for the static wave totals
+    const size_t staged = route_hist_bytes(E) + (((size_t)T * K * sizeof(uint16_t) + 3) & ~(size_t)3);
+    static bool attr_staged = false, attr_plain = false;
+    if (staged <= (size_t)cap) {
+        if (!attr_staged) {
+            hipError_t st = hipFuncSetAttribute((const void*)moe_route_kernel<true>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, cap);
+            if (st != hipSuccess) return st;
+            attr_staged = true;
+        }
+        hipLaunchKernelGGL(moe_route_kernel<true>, dim3(1), dim3(kRouteThreads), staged, stream, idx, T, K, E, BM,
+                           offsets, sorted_pairs, tile_offsets, tile_expert, meta);
+    } else {
+        if (!attr_plain) {
+            hipError_t st = hipFuncSetAttribute((const void*)moe_route_kernel<false>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                (int)route_hist_bytes(kRouteThreads));
+            if (st != hipSuccess) return st;
+            attr_plain = true;
+        }
+        hipLaunchKernelGGL(moe_route_kernel<false>, dim3(1), dim3(kRouteThreads), route_hist_bytes(E), stream, idx, T,
+                           K, E, BM, offsets, sorted_pairs, tile_offsets, tile_expert, meta);
     }
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), lds, stream, idx, T, K, E, BM, offsets,
-                       sorted_pairs, tile_offsets, tile_expert, meta);
     return hipGetLastError();
 }
 

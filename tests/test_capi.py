@@ -38,7 +38,7 @@ def test_workspace_sizes(L):
     assert a >= P * 896 * 2 + P * 1280 * 4  # glu bf16 + staged rows fp32
     assert b > a
     assert L.cernels_moe_experts_workspace_bytes(-1, 1280, 896, 64, 6) == 0
-    assert L.cernels_moe_experts_decode_workspace_bytes(1, 2048, 768, 128, 8) >= 8 * (768 + 2048) * 4
+    assert L.cernels_moe_experts_decode_workspace_bytes(1, 2048, 768, 128, 8) >= 8 * 768 * 2  # glu bf16
     assert L.cernels_moe_route_tile_capacity(2048, 6, 64, 128) == 96 + 64
     assert L.cernels_moe_route_tile_capacity(1, 8, 128, 128) == 1 + 8
 
