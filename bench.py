@@ -232,6 +232,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--report", default=str(ROOT / "gpurun_out" / "bench_report.json"))
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (a known-size kernel against which "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the experts op on one GPU "
@@ -248,6 +251,15 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     hip = _hip()
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[copy calibration] copied {args.copy_calibration_mib} MiB")
+        del src, dst
     if args.configs == "all":
         names = [HEADLINE] + [n for n in BASELINE_ORDER if n != HEADLINE]
     elif args.configs == "headline":

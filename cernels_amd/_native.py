@@ -36,7 +36,8 @@ _SIGNATURES = {
     "cernels_moe_version": (ctypes.c_char_p, []),
     "cernels_moe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "cernels_moe_route_tile_capacity": (_S, [_I, _I, _I, _I]),
-    "cernels_moe_route": (ctypes.c_int, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "cernels_moe_route_workspace_bytes": (_S, [_I, _I, _I]),
+    "cernels_moe_route": (ctypes.c_int, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _S, _P]),
     "cernels_moe_experts_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
     "cernels_moe_experts": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P]),
     "cernels_moe_experts_staged": (

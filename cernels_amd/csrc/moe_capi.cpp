@@ -9,13 +9,15 @@
 namespace cmoe {
 struct GemmParams;
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
-                        int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, hipStream_t stream);
+                        int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
+                        hipStream_t stream);
+size_t route_workspace_bytes(int T, int K, int E);
 int gemm_tile_m();
 hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
-                          int32_t* sorted_pairs, int32_t* tile_expert, int max_tiles, uint16_t* glu, float* Y,
-                          hipStream_t s, hipEvent_t* ev);
+                          int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts, int max_tiles,
+                          uint16_t* glu, float* Y, hipStream_t s, hipEvent_t* ev);
 bool decode_shape_supported(int H, int F);
 int decode_max_pairs();
 int decode_max_tokens();
@@ -33,7 +35,7 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct PrefillWs {
-    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, glu, Y, total;
+    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, route_counts, glu, Y, total;
     int capacity;
 };
 
@@ -48,6 +50,7 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     w.meta = o;         o = align_up(o + sizeof(int32_t) * 4);
     w.sorted_pairs = o; o = align_up(o + sizeof(int32_t) * P);
     w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
+    w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));
     w.glu = o;          o = align_up(o + sizeof(uint16_t) * P * F);
     w.Y = o;            o = align_up(o + sizeof(float) * P * H);
     w.total = o;
@@ -107,6 +110,11 @@ const char* cernels_moe_status_string(int status) {
     }
 }
 
+size_t cernels_moe_route_workspace_bytes(int32_t T, int32_t K, int32_t E) {
+    if (T < 0 || K <= 0 || E <= 0 || (long long)T * K >= (1LL << 31)) return 0;
+    return cmoe::route_workspace_bytes(T, K, E);
+}
+
 size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t tile_m) {
     if (T < 0 || K <= 0 || E <= 0 || tile_m <= 0) return 0;
     const long long P = (long long)T * K;
@@ -116,13 +124,14 @@ size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t 
 
 int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, int32_t tile_m,
                       int32_t* expert_offsets, int32_t* sorted_pairs, int32_t* tile_offsets, int32_t* tile_expert,
-                      int32_t* meta, hipStream_t stream) {
+                      int32_t* meta, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     if (T < 0 || K <= 0 || E <= 0 || E > kMaxExperts || tile_m <= 0 || (long long)T * K >= (1LL << 31))
         return CERNELS_MOE_INVALID_ARGUMENT;
-    if (!expert_offsets || !tile_offsets || !tile_expert || !meta) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (!expert_offsets || !tile_offsets || !tile_expert || !meta || !workspace) return CERNELS_MOE_INVALID_ARGUMENT;
     if (T > 0 && (!indices || !sorted_pairs)) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (workspace_bytes < cmoe::route_workspace_bytes(T, K, E)) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
     return hip_status(cmoe::launch_route(indices, T, K, E, tile_m, expert_offsets, sorted_pairs, tile_offsets,
-                                         tile_expert, meta, stream));
+                                         tile_expert, meta, static_cast<int32_t*>(workspace), stream));
 }
 
 size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K) {
@@ -145,7 +154,8 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
         x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, T, H, F, E, K, layout, act, out,
         reinterpret_cast<int32_t*>(base + w.offsets), reinterpret_cast<int32_t*>(base + w.tile_offsets),
         reinterpret_cast<int32_t*>(base + w.meta), reinterpret_cast<int32_t*>(base + w.sorted_pairs),
-        reinterpret_cast<int32_t*>(base + w.tile_expert), w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
+        reinterpret_cast<int32_t*>(base + w.tile_expert), reinterpret_cast<int32_t*>(base + w.route_counts),
+        w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
         reinterpret_cast<float*>(base + w.Y), stream, stage_events));
 }
 

@@ -19,11 +19,9 @@
 //
 // Tile: 128 rows x 128 B-rows x 64 K per step, 256 threads = 4 waves (2 x 2), each wave a
 // 64 x 64 block of v_mfma_f32_32x32x16_bf16. A and B tiles are staged through LDS with a
-// register double buffer; 16-byte chunks are XOR-swizzled by (row & 7) against bank conflicts.
+// 16-byte chunks XOR-swizzled against LDS bank conflicts (see lds_off).
 // GEMM1's B tile holds 64 gate rows then the 64 matching up rows, so one lane owns the gate and
 // the up value of the same output column and the SwiGLU happens in registers.
-#include <stdlib.h>
-
 #include "moe_common.h"
 
 namespace cmoe {
@@ -58,7 +56,13 @@ struct GemmParams {
     int ldb;                       // row stride of B (elements)
 };
 
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * (kBK * 2) + ((chunk ^ (row & 7)) << 4); }
+// LDS tile layout: row-major 128-byte rows (64 bf16 of K) of eight 16-byte chunks; chunk c of row r
+// sits at chunk c ^ ((r >> 1) & 7). gfx950 LDS serves 256 bytes (64 banks) per clock, i.e. 16
+// lanes of a 16-byte read; the swizzle puts the same chunk of any 16 consecutive rows (two rows per
+// 256-byte bank line) on distinct banks, so MFMA fragment reads (consecutive rows, one chunk) are
+// conflict-free.
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * (kBK * 2) + ((chunk ^ swz(row)) << 4); }
 
 __device__ __forceinline__ u32x4 ld_global_16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -95,28 +99,47 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Multi-stage grouped GEMM for K-contiguous weights (concat layout): A rows (gathered tokens or
-// glu rows) and B rows (weight rows) stream HBM -> LDS directly, STAGES deep, so up to STAGES-1
-// k-steps of loads are in flight while the MFMAs consume the oldest stage. One workgroup of
-// 256 threads per CU (STAGES x 32 KB of LDS).
-template <int MODE, int ACT, bool HAS_BIAS, int STAGES>
-__global__ __launch_bounds__(kGemmThreads, STAGES <= 2 ? 2 : 1) void moe_gemm_dma_kernel(GemmParams prm) {
+// ---- concat-layout grouped GEMM: 128 x 256 tiles, 8 waves, 3-stage direct-to-LDS pipeline ------
+//
+// Weights in the concat layout are K-contiguous ([rows, K]), like the activations, so both operands
+// stream HBM -> LDS with global_load_lds_dwordx4 in the swizzled row layout of lds_off, three
+// k-steps deep (two in flight while the oldest is consumed). 512 threads = 8 waves = two per SIMD,
+// arranged 2 (M) x 4 (N); each wave owns a 64 x 64 block of v_mfma_f32_32x32x16_bf16 results.
+//   GEMM1 (gate_up): the 256 B-rows are 128 gate rows then the 128 matching up rows, so a wave's
+//     two 32-column blocks are the gate and the up value of the same 32 glu columns.
+//   GEMM2 (down): the 256 B-rows are 256 consecutive output columns.
+// Epilogue: the accumulators go through LDS (the pipeline buffers are free by then) so that every
+// row leaves as contiguous 16-byte stores: 256 B of bf16 glu per row, 1 KB of fp32 per output row.
+constexpr int kV3BM = 128;
+constexpr int kV3BN = 256;
+constexpr int kV3Threads = 512;
+constexpr int kV3Waves = kV3Threads / kWave;
+constexpr int kV3Stages = 3;
+constexpr int kV3ABytes = kV3BM * kBK * 2;         // 16 KB
+constexpr int kV3BBytes = kV3BN * kBK * 2;         // 32 KB
+constexpr int kV3StageBytes = kV3ABytes + kV3BBytes;
+constexpr int kV3Lds = kV3Stages * kV3StageBytes;  // 144 KB
+constexpr int kV3APer = kV3BM / 8 / kV3Waves;      // 1 KB copies per wave per stage: A 2, B 4
+constexpr int kV3BPer = kV3BN / 8 / kV3Waves;
+constexpr int kV3CopiesPerStage = kV3APer + kV3BPer;
+constexpr int kV3YStride = kV3BN + 4;              // fp32 epilogue row stride (bank offset per row)
+constexpr int kV3GStride = kV3BN / 2 + 8;          // bf16 epilogue row stride
+
+template <int MODE, int ACT, bool HAS_BIAS>
+__global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams prm) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    constexpr int kStageBytes = 2 * kTileBytes;
-    constexpr int kPer = kBM / 8 / 4;  // 1 KB copies per wave per operand per stage (= 4)
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int wm = wave & 1, wn = wave >> 1;
     const uint32_t lds0 = lds_u32(smem);
+    const int lrow = lane >> 3;
 
     const int tiles = prm.meta[0];
     const int total = tiles * prm.n_tiles;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
     const int per = ceil_div(total, 8);
     const int it_end = min(total, (xcd + 1) * per);
-
-    // lane -> (row within an 8-row group, swizzled 16-byte chunk) of its copies
-    const int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
+    const int halfN = kV3BN / 2;
 
     for (int it = xcd * per + slot; it < it_end; it += slots) {
         const int e = prm.tile_expert[it / prm.n_tiles];
@@ -124,37 +147,41 @@ __global__ __launch_bounds__(kGemmThreads, STAGES <= 2 ? 2 : 1) void moe_gemm_dm
         const int local = it - t0 * prm.n_tiles;
         const int n_idx = local / nt_e, m_idx = local - n_idx * nt_e;
         const int seg0 = prm.offsets[e], seg_n = prm.offsets[e + 1] - seg0;
-        const int row_begin = seg0 + m_idx * kBM;
-        const int rows = min(kBM, seg_n - m_idx * kBM);
-        const int n0 = n_idx * (MODE == kModeGateUp ? kBN / 2 : kBN);
+        const int row_begin = seg0 + m_idx * kV3BM;
+        const int rows = min(kV3BM, seg_n - m_idx * kV3BM);
+        const int n0 = n_idx * (MODE == kModeGateUp ? halfN : kV3BN);  // first output column
         const uint16_t* Be = prm.B + (long long)e * prm.expert_stride;
         const int Kd = prm.Kdim;
 
-        const uint16_t* a_src[kPer];
-        const uint16_t* b_src[kPer];
+        const uint16_t* a_src[kV3APer];
+        const uint16_t* b_src[kV3BPer];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int r = 8 * (i * 4 + wave) + lrow;  // tile row of this lane's copy
+        for (int i = 0; i < kV3APer; ++i) {
+            const int r = 8 * (i * kV3Waves + wave) + lrow;
             const int ra = min(r, rows - 1);
             long long src_row;
             if constexpr (MODE == kModeGateUp) src_row = prm.sorted_pairs[row_begin + ra] / prm.topk;
             else src_row = row_begin + ra;
-            a_src[i] = prm.A + src_row * Kd + lchunk * 8;
+            a_src[i] = prm.A + src_row * Kd + ((lane & 7) ^ swz(r)) * 8;
+        }
+#pragma unroll
+        for (int i = 0; i < kV3BPer; ++i) {
+            const int r = 8 * (i * kV3Waves + wave) + lrow;
             int wrow;
             if constexpr (MODE == kModeGateUp) {
-                const int c = min(n0 + (r & 63), prm.F - 1);
-                wrow = r < 64 ? c : prm.F + c;
+                const int c = min(n0 + (r & (halfN - 1)), prm.F - 1);
+                wrow = r < halfN ? c : prm.F + c;
             } else {
                 wrow = min(n0 + r, prm.N - 1);
             }
-            b_src[i] = Be + (long long)wrow * prm.ldb + lchunk * 8;
+            b_src[i] = Be + (long long)wrow * prm.ldb + ((lane & 7) ^ swz(r)) * 8;
         }
         auto issue = [&](int kt, int stage) {
-            const uint32_t sa = lds0 + stage * kStageBytes + wave * 1024;
+            const uint32_t sa = lds0 + stage * kV3StageBytes + wave * 1024;
 #pragma unroll
-            for (int i = 0; i < kPer; ++i) dma16(a_src[i] + kt * kBK, sa + i * 4096);
+            for (int i = 0; i < kV3APer; ++i) dma16(a_src[i] + kt * kBK, sa + i * (kV3Waves * 1024));
 #pragma unroll
-            for (int i = 0; i < kPer; ++i) dma16(b_src[i] + kt * kBK, sa + kTileBytes + i * 4096);
+            for (int i = 0; i < kV3BPer; ++i) dma16(b_src[i] + kt * kBK, sa + kV3ABytes + i * (kV3Waves * 1024));
         };
 
         f32x16 acc[2][2];
@@ -168,7 +195,7 @@ __global__ __launch_bounds__(kGemmThreads, STAGES <= 2 ? 2 : 1) void moe_gemm_dm
         int brow[2];
         if constexpr (MODE == kModeGateUp) {
             brow[0] = wn * 32;
-            brow[1] = 64 + wn * 32;
+            brow[1] = halfN + wn * 32;
         } else {
             brow[0] = wn * 64;
             brow[1] = wn * 64 + 32;
@@ -177,23 +204,17 @@ __global__ __launch_bounds__(kGemmThreads, STAGES <= 2 ? 2 : 1) void moe_gemm_dm
         const int khalf = lane >> 5;
         const int nk = Kd / kBK;
 
-        wait_vmcnt<0>();  // the index loads above must not be counted against the copies below
+        wait_vmcnt<0>();  // index loads above must not be counted against the copies below
 #pragma unroll
-        for (int s = 0; s < STAGES - 1; ++s)
+        for (int s = 0; s < kV3Stages - 1; ++s)
             if (s < nk) issue(s, s);
         for (int kt = 0; kt < nk; ++kt) {
-            // copies of stages kt+1 .. min(kt+STAGES-2, nk-1) may stay in flight
-            const int younger = min(STAGES - 2, nk - 1 - kt);
-            if (younger >= STAGES - 2) wait_vmcnt<2 * kPer * (STAGES - 2)>();
-            else if (STAGES >= 4 && younger == 2) wait_vmcnt<2 * kPer * 2>();
-            else if (STAGES >= 3 && younger == 1) wait_vmcnt<2 * kPer>();
+            if (kt + 1 < nk) wait_vmcnt<kV3CopiesPerStage>();  // stage kt+1 may stay in flight
             else wait_vmcnt<0>();
             __syncthreads();
-            if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-            const unsigned char* sA = smem + (kt % STAGES) * kStageBytes;
-            const unsigned char* sB = sA + kTileBytes;
-            // all 16 fragments of this k-step first, so the MFMAs of sub-step ks overlap the LDS
-            // reads of the later sub-steps
+            if (kt + kV3Stages - 1 < nk) issue(kt + kV3Stages - 1, (kt + kV3Stages - 1) % kV3Stages);
+            const unsigned char* sA = smem + (kt % kV3Stages) * kV3StageBytes;
+            const unsigned char* sB = sA + kV3ABytes;
             bf16x8 af[kBK / 16][2], bfr[kBK / 16][2];
 #pragma unroll
             for (int ks = 0; ks < kBK / 16; ++ks) {
@@ -214,52 +235,66 @@ __global__ __launch_bounds__(kGemmThreads, STAGES <= 2 ? 2 : 1) void moe_gemm_dm
                         acc[mb][nb] =
                             __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][mb], bfr[ks][nb], acc[mb][nb], 0, 0, 0);
         }
+        __syncthreads();  // all waves are done reading the pipeline buffers; reuse them for the epilogue
 
+        // ---- epilogue through LDS. Accumulator element r of a 32x32 block sits at
+        // row 8*(r/4) + 4*(lane/32) + (r%4), column lane & 31.
         if constexpr (MODE == kModeGateUp) {
-            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            const int n = n0 + wn * 32 + (lane & 31);
-            if (n < prm.N) {
-                float bg = 0.f, bu = 0.f;
-                if constexpr (HAS_BIAS) {
-                    const float* be = prm.bias + (long long)e * 2 * prm.F;
-                    bg = be[n];
-                    bu = be[prm.F + n];
-                }
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (row < rows) {
-                            const float v = swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu);
-                            glu[(long long)(row_begin + row) * prm.F + n] = f32_to_bf16_bits(v);
-                        }
-                    }
+            uint16_t* stg = reinterpret_cast<uint16_t*>(smem);  // [128][kV3GStride] bf16 glu tile
+            const int c = wn * 32 + (lane & 31);                 // glu column within the tile
+            float bg = 0.f, bu = 0.f;
+            if constexpr (HAS_BIAS) {
+                const int n = min(n0 + c, prm.F - 1);
+                bg = prm.bias[(long long)e * 2 * prm.F + n];
+                bu = prm.bias[(long long)e * 2 * prm.F + prm.F + n];
             }
-        } else {
-            float* Y = reinterpret_cast<float*>(prm.out);
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < rows) {
-                        const int p = prm.sorted_pairs[row_begin + row];
-                        const float w = prm.route_w[p];
+                    stg[row * kV3GStride + c] = f32_to_bf16_bits(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu));
+                }
+            __syncthreads();
+            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+            constexpr int kChunks = kV3BN / 2 / 8;  // 16-byte chunks per glu row (16)
+            for (int i = tid; i < kV3BM * kChunks; i += kV3Threads) {
+                const int row = i / kChunks, ch = i - row * kChunks;
+                const int n = n0 + ch * 8;
+                if (row < rows && n < prm.N)
+                    *reinterpret_cast<u32x4*>(glu + (long long)(row_begin + row) * prm.F + n) =
+                        *reinterpret_cast<const u32x4*>(stg + row * kV3GStride + ch * 8);
+            }
+        } else {
+            float* stg = reinterpret_cast<float*>(smem);  // [128][kV3YStride] fp32 tile
 #pragma unroll
-                        for (int nb = 0; nb < 2; ++nb) {
-                            const int n = n0 + brow[nb] + (lane & 31);
-                            if (n < prm.N) {
-                                float v = acc[mb][nb][r];
-                                if constexpr (HAS_BIAS) v += prm.bias[(long long)e * prm.N + n];
-                                Y[(long long)p * prm.N + n] = v * w;
-                            }
-                        }
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        stg[row * kV3YStride + brow[nb] + (lane & 31)] = acc[mb][nb][r];
                     }
+            __syncthreads();
+            float* Y = reinterpret_cast<float*>(prm.out);
+            constexpr int kChunks = kV3BN / 4;  // 16-byte chunks per output row (64)
+            for (int i = tid; i < kV3BM * kChunks; i += kV3Threads) {
+                const int row = i / kChunks, ch = i - row * kChunks;
+                const int n = n0 + ch * 4;
+                if (row < rows && n < prm.N) {
+                    const int p = prm.sorted_pairs[row_begin + row];
+                    const float w = prm.route_w[p];
+                    f32x4 v = *reinterpret_cast<const f32x4*>(stg + row * kV3YStride + ch * 4);
+                    if constexpr (HAS_BIAS) {
+                        const f32x4 b = *reinterpret_cast<const f32x4*>(prm.bias + (long long)e * prm.N + n);
+                        v += b;
+                    }
+                    *reinterpret_cast<f32x4*>(Y + (long long)p * prm.N + n) = v * w;
                 }
             }
         }
-        __syncthreads();  // every wave is done with the LDS stages before the next item's copies
+        __syncthreads();  // the staging tile is reused by the next item's copies
     }
 }
 
@@ -496,34 +531,18 @@ static int cu_count() {
 
 int gemm_tile_m() { return kBM; }
 
-// LDS pipeline depth of the concat-layout GEMM: 2 stages (64 KB, two workgroups per CU) by
-// default — measured faster on MI355X than 3 or 4 stages with one workgroup per CU, because the
-// second workgroup covers the first one's item prologue and epilogue. CERNELS_GEMM_STAGES=3|4
-// selects the deeper single-workgroup pipelines.
-static int gemm_stages() {
-    static int stages = 0;
-    if (stages == 0) {
-        const char* v = getenv("CERNELS_GEMM_STAGES");
-        const int s = v ? atoi(v) : 2;
-        stages = (s == 3 || s == 4) ? s : 2;
-    }
-    return stages;
-}
-
-template <int MODE, int ACT, bool HAS_BIAS, int STAGES>
-static hipError_t launch_dma_t(const GemmParams& prm, int upper, hipStream_t stream) {
+template <int MODE, int ACT, bool HAS_BIAS>
+static hipError_t launch_v3_t(const GemmParams& prm, int upper, hipStream_t stream) {
     static bool attr = false;
-    const size_t lds = (size_t)STAGES * 2 * kTileBytes;
     if (!attr) {
-        hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_dma_kernel<MODE, ACT, HAS_BIAS, STAGES>,
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_v3_kernel<MODE, ACT, HAS_BIAS>,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, kV3Lds);
         if (st != hipSuccess) return st;
         attr = true;
     }
-    int grid = min(upper, cu_count() * (STAGES <= 2 ? 2 : 1));
+    int grid = min(upper, cu_count());
     grid = ceil_div(max(grid, 1), 8) * 8;
-    hipLaunchKernelGGL((moe_gemm_dma_kernel<MODE, ACT, HAS_BIAS, STAGES>), dim3(grid), dim3(kGemmThreads), lds, stream,
-                       prm);
+    hipLaunchKernelGGL((moe_gemm_v3_kernel<MODE, ACT, HAS_BIAS>), dim3(grid), dim3(kV3Threads), kV3Lds, stream, prm);
     return hipGetLastError();
 }
 
@@ -531,11 +550,7 @@ template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
 static hipError_t launch_gemm_t(const GemmParams& prm, int max_tiles, hipStream_t stream) {
     const int upper = max_tiles * prm.n_tiles;
     if constexpr (LAYOUT == kLayoutConcat) {
-        switch (gemm_stages()) {
-            case 2: return launch_dma_t<MODE, ACT, HAS_BIAS, 2>(prm, upper, stream);
-            case 3: return launch_dma_t<MODE, ACT, HAS_BIAS, 3>(prm, upper, stream);
-            default: return launch_dma_t<MODE, ACT, HAS_BIAS, 4>(prm, upper, stream);
-        }
+        return launch_v3_t<MODE, ACT, HAS_BIAS>(prm, upper, stream);
     } else {
         int grid = min(upper, cu_count() * 2);
         grid = ceil_div(max(grid, 1), 8) * 8;
@@ -577,20 +592,22 @@ hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int
 }
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
-                        int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, hipStream_t stream);
+                        int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
+                        hipStream_t stream);
 
 // route -> gate_up GEMM -> down GEMM -> combine, all on stream s. Shapes were checked by the caller
 // (H % 64 == 0, F % 64 == 0, E <= 1024, T >= 1).
 hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
-                          int32_t* sorted_pairs, int32_t* tile_expert, int max_tiles, uint16_t* glu, float* Y,
-                          hipStream_t s, hipEvent_t* ev) {
+                          int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts, int max_tiles,
+                          uint16_t* glu, float* Y, hipStream_t s, hipEvent_t* ev) {
     // ev (optional): 5 events recorded before route, after route, after gate_up, after down,
     // after combine — for per-stage timing on the caller's stream.
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     mark(0);
-    hipError_t st = launch_route(idx, T, K, E, kBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, s);
+    hipError_t st =
+        launch_route(idx, T, K, E, kBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts, s);
     if (st != hipSuccess) return st;
     mark(1);
     const bool concat = layout == kLayoutConcat;
@@ -609,7 +626,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g1.N = F;
     g1.F = F;
     g1.topk = K;
-    g1.n_tiles = ceil_div(F, kBN / 2);
+    g1.n_tiles = concat ? ceil_div(F, kV3BN / 2) : ceil_div(F, kBN / 2);
     g1.expert_stride = 2LL * F * H;
     g1.ldb = concat ? H : 2 * F;
     st = launch_gateup(g1, layout, act, b1 != nullptr, max_tiles, s);
@@ -622,7 +639,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g2.out = Y;
     g2.Kdim = F;
     g2.N = H;
-    g2.n_tiles = ceil_div(H, kBN);
+    g2.n_tiles = concat ? ceil_div(H, kV3BN) : ceil_div(H, kBN);
     g2.expert_stride = (long long)H * F;
     g2.ldb = concat ? F : H;
     st = launch_down(g2, layout, b2 != nullptr, max_tiles, s);

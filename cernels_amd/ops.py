@@ -132,9 +132,11 @@ def route(indices: torch.Tensor, num_experts: int, tile_m: int = 128):
     toff = torch.empty(num_experts + 1, **i32)
     texp = torch.full((max(cap, 1),), -1, **i32)
     meta = torch.empty(2, **i32)
+    nbytes = max(int(L.cernels_moe_route_workspace_bytes(T, K, num_experts)), 4)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = L.cernels_moe_route(_ptr(indices), T, K, num_experts, tile_m, _ptr(offsets), _ptr(pairs), _ptr(toff),
-                                 _ptr(texp), _ptr(meta), _stream(dev))
+                                 _ptr(texp), _ptr(meta), _ptr(ws), ctypes.c_size_t(nbytes), _stream(dev))
     check(st, "cernels_moe_route")
     return offsets, pairs[: T * K], toff, texp, meta
 

@@ -63,11 +63,14 @@ const char* cernels_moe_status_string(int status);
  *   tile_offsets   [E+1]: exclusive scan of ceil(count_e / tile_m).
  *   tile_expert    [cernels_moe_route_tile_capacity()]: expert of each M-tile.
  *   meta           [2]  : meta[0] = number of M-tiles, meta[1] = valid pairs.
+ *   workspace      scratch of cernels_moe_route_workspace_bytes() (per-tile expert counts).
  * Limits: 1 <= E <= 1024, T*K < 2^31, tile_m >= 1. */
 size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t tile_m);
+size_t cernels_moe_route_workspace_bytes(int32_t T, int32_t K, int32_t E);
 int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, int32_t tile_m,
                       int32_t* expert_offsets, int32_t* sorted_pairs, int32_t* tile_offsets,
-                      int32_t* tile_expert, int32_t* meta, hipStream_t stream);
+                      int32_t* tile_expert, int32_t* meta, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
 
 /* ---- prefill: grouped GEMM experts ------------------------------------------------------------
  * route -> gate_up GEMM (+bias, SwiGLU in the epilogue) -> down GEMM (+bias, x routing weight in

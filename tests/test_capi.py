@@ -73,10 +73,14 @@ def test_null_pointers_rejected(L):
     st = L.cernels_moe_experts(None, p, None, p, None, p, p, 4, 128, 64, 8, 2, 0, 0, p, p, ctypes.c_size_t(1 << 30),
                                None)
     assert st == 1
-    st = L.cernels_moe_route(None, 4, 2, 8, 128, p, p, p, p, p, None)
+    big = ctypes.c_size_t(1 << 20)
+    st = L.cernels_moe_route(None, 4, 2, 8, 128, p, p, p, p, p, p, big, None)
     assert st == 1
-    st = L.cernels_moe_route(p, 4, 2, 2048, 128, p, p, p, p, p, None)
+    st = L.cernels_moe_route(p, 4, 2, 2048, 128, p, p, p, p, p, p, big, None)
     assert st == 1  # E > 1024
+    st = L.cernels_moe_route(p, 4096, 10, 512, 128, p, p, p, p, p, p, ctypes.c_size_t(16), None)
+    assert st == 4  # workspace too small
+    assert L.cernels_moe_route_workspace_bytes(4096, 10, 512) == 40 * 512 * 4
 
 
 def test_per_model_entries_check_arguments(L):
