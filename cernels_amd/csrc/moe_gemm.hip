@@ -91,7 +91,7 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
     return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const unsigned char*)(p));
 }
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds) : "memory");
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds) : "memory", "m0");
 }
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
