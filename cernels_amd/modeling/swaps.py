@@ -1,85 +1,99 @@
-"""Per-model expert swaps: replace ``forward`` on every experts instance of a loaded model.
+"""Instance-level expert swaps: route a loaded model's experts modules through this library.
 
-Mirrors src/modeling/swaps.py:13-65 of the reference for its MoE-experts half. ``apply(model,
-variant)`` mutates the model in place; ``"stock"`` deletes the instance attribute, restoring the
-class method. Variants: ``stock`` → ``custom_prefill`` (prefill entry only) → ``custom``
-(prefill + decode entries).
+Contract kept from the reference (src/modeling/swaps.py:20-53): an experts module is called as
+``module(hidden, top_k_index, top_k_weights)``; a swapped module instead calls
+``op(hidden, top_k_index, top_k_weights, module)`` where ``op`` is a registry loader's
+``kernel`` (prefill) or ``decode_kernel`` (few tokens). ``apply(model, variant)`` edits the
+model in place and ``"stock"`` restores the class forward. Variants per model are listed in
+``SWAPS`` in sweep order, stock first. Only the MoE-experts part of the reference's swaps is
+here; its SAM rel-pos and vision-tower variants are other kernels.
 
-The decode entry handles calls with at most ``DECODE_MAX_TOKENS`` tokens. The reference uses 4
-(swaps.py:13); the gfx950 decode GEMV streams each distinct expert once and stays ahead of the
-grouped GEMM to well above that, so the threshold here covers the 8-token decode workload too.
+Decode dispatch: calls with at most ``DECODE_MAX_TOKENS`` tokens use the decode GEMV. The
+reference switches at 4 (swaps.py:13). The gfx950 GEMV streams every distinct selected expert
+once, so it stays the faster entry up to the 8-token decode workload; the threshold is 8.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+from importlib import import_module
+
 DECODE_MAX_TOKENS = 8
 
-
-def _experts_fwd(mod, kernel, decode_kernel):
-    def fwd(h, idx, w, _m=mod):
-        op = decode_kernel if h.size(0) <= DECODE_MAX_TOKENS else kernel
-        if op is None:  # this shape's entry point is not enabled in this variant
-            return type(_m).forward(_m, h, idx, w)
-        return op(h, idx, w, _m)
-
-    return fwd
+_REG = "cernels_amd.kops.registry."
 
 
-def _swap_experts(model, cls_name, kernel, decode_kernel):
-    """Set (or, with both kernels None, restore) the forward on every ``cls_name`` instance."""
-    n = 0
-    for mod in model.modules():
-        if type(mod).__name__ != cls_name:
-            continue
-        n += 1
-        if "forward" in vars(mod):
-            del mod.forward
-        if kernel is not None or decode_kernel is not None:
-            mod.forward = _experts_fwd(mod, kernel, decode_kernel)
-    if not n:
-        raise RuntimeError(f"no {cls_name} modules found — wrong model for this swap")
-    return n
+@dataclass(frozen=True)
+class ExpertSwap:
+    """Which experts class to patch and which loader module supplies ``kernel``/``decode_kernel``."""
+
+    experts_class: str
+    loader: str
+    variants: tuple[str, ...]
 
 
-def north_mini_code(model, variant):
-    from cernels_amd.kops.registry.cohere2_moe_experts import decode_kernel, kernel
-
-    return _swap_experts(
-        model,
-        "Cohere2MoeExperts",
-        None if variant == "stock" else kernel,
-        decode_kernel if variant == "custom" else None,
-    )
-
-
-def deepseek_ocr_2(model, variant):
-    """MoE half of the reference's deepseek_ocr_2 swap (swaps.py:56-65); the SAM rel-pos and
-    vision-tower variants of that function are outside the MoE-experts path."""
-    from cernels_amd.kops.registry.deepseek_ocr2_moe_experts import decode_kernel, kernel
-
-    moe = variant != "stock"
-    return _swap_experts(
-        model,
-        "DeepseekOcr2TextExperts",
-        kernel if moe else None,
-        decode_kernel if moe else None,
-    )
-
-
-def qwen3_next(model, variant):
-    """Qwen3NextExperts swap (prefill entry; the reference has no qwen3 decode entry)."""
-    from cernels_amd.kops.registry.cohere2_moe_experts import decode_kernel, kernel
-
-    return _swap_experts(
-        model,
-        "Qwen3NextExperts",
-        None if variant == "stock" else kernel,
-        decode_kernel if variant == "custom" else None,
-    )
-
-
-SWAPS = {
-    "north_mini_code": (north_mini_code, ("stock", "custom_prefill", "custom")),
-    "deepseek_ocr_2": (deepseek_ocr_2, ("stock", "custom")),
-    "qwen3_next": (qwen3_next, ("stock", "custom_prefill", "custom")),
+SWAP_TABLE = {
+    "north_mini_code": ExpertSwap("Cohere2MoeExperts", "cohere2_moe_experts", ("stock", "custom_prefill", "custom")),
+    "deepseek_ocr_2": ExpertSwap("DeepseekOcr2TextExperts", "deepseek_ocr2_moe_experts", ("stock", "custom")),
+    # Qwen3NextExperts has the concat layout and plain SwiGLU of the cohere2 op.
+    "qwen3_next": ExpertSwap("Qwen3NextExperts", "cohere2_moe_experts", ("stock", "custom_prefill", "custom")),
 }
+
+
+def entry_points(model_name: str, variant: str):
+    """(prefill op, decode op) that ``variant`` enables; ``None`` keeps the module's own forward."""
+    spec = SWAP_TABLE[model_name]
+    if variant not in spec.variants:
+        raise KeyError(f"{model_name}: unknown variant {variant!r}; known: {spec.variants}")
+    if variant == "stock":
+        return None, None
+    loader = import_module(_REG + spec.loader)
+    decode_on = variant == "custom"
+    return loader.kernel, (loader.decode_kernel if decode_on else None)
+
+
+def _dispatching_forward(module, prefill_op, decode_op):
+    stock = type(module).forward
+
+    def forward(hidden, top_k_index, top_k_weights):
+        op = decode_op if hidden.size(0) <= DECODE_MAX_TOKENS else prefill_op
+        if op is None:
+            return stock(module, hidden, top_k_index, top_k_weights)
+        return op(hidden, top_k_index, top_k_weights, module)
+
+    return forward
+
+
+def install(model, experts_class: str, prefill_op, decode_op) -> int:
+    """Patch (or, with both ops None, restore) ``forward`` on every ``experts_class`` instance.
+
+    Returns the number of modules touched; raises if the model has none.
+    """
+    targets = [m for m in model.modules() if type(m).__name__ == experts_class]
+    if not targets:
+        raise RuntimeError(f"no {experts_class} modules in this model; wrong swap for it")
+    for m in targets:
+        vars(m).pop("forward", None)
+        if prefill_op is not None or decode_op is not None:
+            m.forward = _dispatching_forward(m, prefill_op, decode_op)
+    return len(targets)
+
+
+def apply(model, model_name: str, variant: str) -> int:
+    prefill_op, decode_op = entry_points(model_name, variant)
+    return install(model, SWAP_TABLE[model_name].experts_class, prefill_op, decode_op)
+
+
+def _model_swap(model_name: str):
+    def swap(model, variant):
+        return apply(model, model_name, variant)
+
+    swap.__name__ = model_name
+    return swap
+
+
+# name -> (apply(model, variant), variants), the shape of the reference's SWAPS table.
+SWAPS = {name: (_model_swap(name), spec.variants) for name, spec in SWAP_TABLE.items()}
+north_mini_code = SWAPS["north_mini_code"][0]
+deepseek_ocr_2 = SWAPS["deepseek_ocr_2"][0]
+qwen3_next = SWAPS["qwen3_next"][0]
