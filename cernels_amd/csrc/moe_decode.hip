@@ -2,18 +2,17 @@
 //
 // Replaces decode_gateup_swiglu_kernel / decode_down_accum_kernel + zeros + cast
 // (src/kops/cohere2_moe_experts/csrc/cohere2_moe_experts.cu:135-236). Differences by design:
-//   * work is split by DISTINCT expert, so an expert picked by several (token, slot) pairs
-//     streams its weights from HBM once (the reference streams them once per pair, .cu:143,179);
-//   * 64-lane waves read 16-byte chunks of a weight row (1 KB per wave instruction);
+//   * the gate_up GEMV is split by DISTINCT expert, so an expert picked by several
+//     (token, slot) pairs streams its gate_up rows from HBM once (the reference streams them once
+//     per pair, .cu:143);
+//   * 64-lane waves read whole 1 KB runs of a weight row per instruction (16 bytes per lane) and
+//     keep every row they own in flight at once; dot products use v_dot2c_f32_bf16;
 //   * the top-k combine is fused into the down GEMV: a workgroup owns whole output rows and sums
-//     every (expert, pair) contribution for them in a fixed order, then writes bf16 — no fp32
+//     every (token, slot) contribution for them in a fixed order, then writes bf16 — no fp32
 //     atomics, no cross-workgroup synchronisation, no zero-fill or cast kernel. Two launches.
 //
 // Layout: concat only (gate_up [E, 2F, H], down [E, H, F]); the reference has no decode entry
 // for the interleaved gpt-oss layout either.
-//
-// Each workgroup rebuilds the routing plan for the <= 256 pairs in LDS: the distinct experts in
-// ascending order and, per expert, its pairs in (slot, token) order.
 #include "moe_common.h"
 
 namespace cmoe {
@@ -22,58 +21,27 @@ constexpr int kDecThreads = 256;
 constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kDecMaxPairs = 256;
 constexpr int kDecMaxTokens = 64;
-constexpr int kDecRowsPerWaveG = 2;   // gate_up kernel: F rows per wave (each = a gate and an up row)
-constexpr int kDecRowsPerWaveD = 4;   // down kernel: H rows per workgroup (every wave holds all 4)
-constexpr int kDecFBlock = kDecWaves * kDecRowsPerWaveG;  // 8
+constexpr int kDecMaxExperts = 1024;  // bitmap of 32 words
+constexpr int kDecDownRows = 2;       // output rows per down workgroup
 
-struct DecodePlan {
-    int e[kDecMaxPairs];       // expert of pair p, -1 if out of range
-    int spair[kDecMaxPairs];   // pairs in (expert, slot, token) order
-    int dexp[kDecMaxPairs];    // distinct experts, ascending
-    int dstart[kDecMaxPairs + 1];
-    int first[kDecMaxPairs];
-    int U;
-};
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__device__ void build_plan(DecodePlan& pl, const int32_t* __restrict__ idx, int T, int K, int E) {
-    const int P = T * K, tid = threadIdx.x;
-    for (int p = tid; p < P; p += kDecThreads) {
-        const int v = idx[p];
-        pl.e[p] = ((unsigned)v < (unsigned)E) ? v : -1;
-    }
-    __syncthreads();
-    int less = 0;
-    const int p = tid;  // P <= kDecThreads is checked on the host
-    const int ep = p < P ? pl.e[p] : -1;
-    if (ep >= 0) {
-        const int key = (p % K) * T + p / K;
-        int same_before = 0;
-        for (int q = 0; q < P; ++q) {
-            const int eq = pl.e[q];
-            if (eq < 0) continue;
-            if (eq < ep) ++less;
-            else if (eq == ep && (q % K) * T + q / K < key) ++same_before;
-        }
-        pl.spair[less + same_before] = p;
-        pl.first[p] = same_before == 0;
-    } else if (p < P) {
-        pl.first[p] = 0;
-    }
-    const int nvalid = __syncthreads_count(ep >= 0);
-    const int U = __syncthreads_count(p < P && pl.first[p]);
-    if (p < P && pl.first[p]) {
-        int u = 0;
-        for (int q = 0; q < P; ++q) u += (pl.first[q] && pl.e[q] < ep);
-        pl.dexp[u] = ep;
-        pl.dstart[u] = less;
-    }
-    if (tid == 0) {
-        pl.dstart[U] = nvalid;
-        pl.U = U;
-    }
-    __syncthreads();
+// 8-element bf16 dot product, fp32 accumulate. The vectors are reinterpreted whole and split with
+// shufflevector: a bit_cast of a single vector-element lvalue (a[d]) reads element 0 whatever d is.
+__device__ __forceinline__ float dot8(const u32x4& a, const u32x4& b, float acc) {
+    const bf16x8 av = __builtin_bit_cast(bf16x8, a), bv = __builtin_bit_cast(bf16x8, b);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 0, 1), __builtin_shufflevector(bv, bv, 0, 1),
+                                          acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 2, 3), __builtin_shufflevector(bv, bv, 2, 3),
+                                          acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 4, 5), __builtin_shufflevector(bv, bv, 4, 5),
+                                          acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(av, av, 6, 7), __builtin_shufflevector(bv, bv, 6, 7),
+                                          acc, false);
+    return acc;
 }
 
+// Lane-strided row chunks: lane l holds 16-byte chunks l, l+64, ... of a row of nch chunks.
 template <int MAXC>
 __device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int nch, int lane, u32x4 (&v)[MAXC]) {
 #pragma unroll
@@ -84,134 +52,195 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int n
     }
 }
 
-__device__ __forceinline__ float dot8_bf16(const u32x4& a, const u32x4& b, float acc) {
+// Sum of N per-lane values over the wave, several values per exchange: after the halving steps
+// (offsets 32, 16, ... while more than G values remain), each lane holds G values that are sums over
+// the lanes sharing its upper bits; the remaining single-offset steps complete those G sums in every
+// lane. On return, v[0..G) of lane l hold totals of the value group selected by l's upper bits:
+// group index = lane >> (6 - log2(N/G)).
+template <int N, int G>
+__device__ __forceinline__ void wave_reduce_groups(float (&v)[N], int lane) {
+    int n = N, o = 32;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        acc = fmaf(bf16_lo(a[d]), bf16_lo(b[d]), acc);
-        acc = fmaf(bf16_hi(a[d]), bf16_hi(b[d]), acc);
+    for (; n > G; n >>= 1, o >>= 1) {
+        const bool upper = lane & o;
+#pragma unroll
+        for (int i = 0; i < n / 2; ++i) {
+            const float send = upper ? v[i] : v[i + n / 2];
+            const float keep = upper ? v[i + n / 2] : v[i];
+            v[i] = keep + __shfl_xor(send, o, kWave);
+        }
     }
-    return acc;
+#pragma unroll
+    for (; o > 0; o >>= 1)
+#pragma unroll
+        for (int i = 0; i < G; ++i) v[i] += __shfl_xor(v[i], o, kWave);
 }
 
-__device__ __forceinline__ float dot8_bf16_f32(const u32x4& w, const f32x4& g0, const f32x4& g1, float acc) {
-    acc = fmaf(bf16_lo(w[0]), g0[0], acc);
-    acc = fmaf(bf16_hi(w[0]), g0[1], acc);
-    acc = fmaf(bf16_lo(w[1]), g0[2], acc);
-    acc = fmaf(bf16_hi(w[1]), g0[3], acc);
-    acc = fmaf(bf16_lo(w[2]), g1[0], acc);
-    acc = fmaf(bf16_hi(w[2]), g1[1], acc);
-    acc = fmaf(bf16_lo(w[3]), g1[2], acc);
-    acc = fmaf(bf16_hi(w[3]), g1[3], acc);
-    return acc;
-}
-
-// glu[p, f] = bf16(act(x[t] . W1_e[f] + b, x[t] . W1_e[F+f] + b)) for every pair p of expert e.
-// grid: (ceil(F / 8), P); blockIdx.y = distinct-expert slot. Each wave owns 2 consecutive f and
-// keeps their 4 weight rows (2 gate + 2 up) in flight at once.
-template <int ACT, bool HAS_BIAS, int MAXC>
+// glu[p, f] = bf16(act(x[t_p] . W1_e[f] + b1_e[f], x[t_p] . W1_e[F+f] + b1_e[F+f])) for the pairs p
+// of one distinct expert e.
+// grid: (ceil(F / (4 * R)), min(T*K, E)); blockIdx.y = u picks the u-th smallest distinct expert
+// (workgroups past the number of distinct experts return at once). Wave w owns R consecutive f and
+// keeps their 2R weight rows in registers for all of e's pairs.
+template <int ACT, bool HAS_BIAS, int MAXC, int R>
 __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1, const float* __restrict__ b1,
     const int32_t* __restrict__ idx, uint16_t* __restrict__ glu, int T, int H, int F, int E, int K) {
-    __shared__ DecodePlan pl;
-    build_plan(pl, idx, T, K, E);
-    const int u = blockIdx.y;
-    if (u >= pl.U) return;
-    const int e = pl.dexp[u], ps = pl.dstart[u], pe = pl.dstart[u + 1];
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int nch = H / 8;
-    const uint16_t* we = w1 + (long long)e * 2 * F * H;
-    const int f0 = blockIdx.x * kDecFBlock + wave * kDecRowsPerWaveG;
-    if (f0 >= F) return;
-    const int f1 = min(f0 + 1, F - 1);
-    u32x4 wg0[MAXC], wu0[MAXC], wg1[MAXC], wu1[MAXC];
-    load_row<MAXC>(we + (long long)f0 * H, nch, lane, wg0);
-    load_row<MAXC>(we + (long long)(F + f0) * H, nch, lane, wu0);
-    load_row<MAXC>(we + (long long)f1 * H, nch, lane, wg1);
-    load_row<MAXC>(we + (long long)(F + f1) * H, nch, lane, wu1);
-    float bg0 = 0.f, bu0 = 0.f, bg1 = 0.f, bu1 = 0.f;
-    if constexpr (HAS_BIAS) {
-        const float* be = b1 + (long long)e * 2 * F;
-        bg0 = be[f0], bu0 = be[F + f0], bg1 = be[f1], bu1 = be[F + f1];
+    __shared__ uint32_t bits[kDecMaxExperts / 32];
+    __shared__ int s_e, s_np;
+    __shared__ int s_wcnt[kDecWaves];
+    __shared__ int s_pairs[kDecMaxPairs];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int P = T * K, u = blockIdx.y;
+
+    // ---- which expert: the u-th set bit of the bitmap of valid expert ids
+    if (tid < kDecMaxExperts / 32) bits[tid] = 0u;
+    int ep = -1;
+    if (tid < P) {  // P <= 256 is checked on the host
+        const int v = idx[tid];
+        ep = ((unsigned)v < (unsigned)E) ? v : -1;
     }
-    for (int s = ps; s < pe; ++s) {
-        const int p = pl.spair[s];
+    __syncthreads();
+    if (ep >= 0) atomicOr(&bits[ep >> 5], 1u << (ep & 31));
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t w = lane < kDecMaxExperts / 32 ? bits[lane] : 0u;
+        const int c = __popc(w);
+        int incl = c;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int y = __shfl_up(incl, o, kWave);
+            if (lane >= o) incl += y;
+        }
+        const int excl = incl - c;
+        if (lane == 0) s_e = -1;
+        __builtin_amdgcn_wave_barrier();
+        if (u >= excl && u < incl) {  // at most one lane
+            for (int r = u - excl; r > 0; --r) w &= w - 1;
+            s_e = lane * 32 + __ffs(w) - 1;
+        }
+    }
+    __syncthreads();
+    const int e = s_e;
+    if (e < 0) return;  // uniform: fewer distinct experts than u + 1
+
+    // ---- start streaming this wave's 2R weight rows before building the pair list
+    const int nch = H / 8;
+    const int f0 = (blockIdx.x * kDecWaves + wave) * R;
+    const uint16_t* we = w1 + (long long)e * 2 * F * H;
+    u32x4 wr[2 * R][MAXC];  // rows: gate f0, up f0, gate f0+1, up f0+1, ...
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int f = min(f0 + r, F - 1);
+        load_row<MAXC>(we + (long long)f * H, nch, lane, wr[2 * r]);
+        load_row<MAXC>(we + (long long)(F + f) * H, nch, lane, wr[2 * r + 1]);
+    }
+
+    // ---- pairs of e, ascending p
+    const bool mine = ep == e;
+    const uint64_t ball = __ballot(mine);
+    if (lane == 0) s_wcnt[wave] = __popcll(ball);
+    __syncthreads();
+    int base = 0;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) base += w < wave ? s_wcnt[w] : 0;
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    if (mine) s_pairs[base + __popcll(ball & lt)] = tid;
+    if (tid == 0) s_np = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+    __syncthreads();
+    if (f0 >= F) return;
+
+    // after the reduction, lane group r (the upper log2(R) lane bits) holds the gate/up sums of f0 + r
+    constexpr int gr_shift = 6 - (R == 1 ? 0 : (R == 2 ? 1 : (R == 4 ? 2 : 3)));
+    const int my_r = lane >> gr_shift;
+    float bg = 0.f, bu = 0.f;
+    if constexpr (HAS_BIAS) {
+        const int f = min(f0 + my_r, F - 1);
+        bg = b1[(long long)e * 2 * F + f];
+        bu = b1[(long long)e * 2 * F + F + f];
+    }
+    const bool writer = (lane & ((1 << gr_shift) - 1)) == 0 && f0 + my_r < F;
+    const int np = s_np;
+    for (int s = 0; s < np; ++s) {
+        const int p = s_pairs[s];
         const int t = p / K;
         u32x4 xv[MAXC];
         load_row<MAXC>(x + (long long)t * H, nch, lane, xv);
-        float g0 = 0.f, u0 = 0.f, g1 = 0.f, u1 = 0.f;
+        float v[2 * R];
 #pragma unroll
-        for (int i = 0; i < MAXC; ++i) {
-            g0 = dot8_bf16(wg0[i], xv[i], g0);
-            u0 = dot8_bf16(wu0[i], xv[i], u0);
-            g1 = dot8_bf16(wg1[i], xv[i], g1);
-            u1 = dot8_bf16(wu1[i], xv[i], u1);
+        for (int j = 0; j < 2 * R; ++j) {
+            v[j] = 0.f;
+#pragma unroll
+            for (int i = 0; i < MAXC; ++i) v[j] = dot8(wr[j][i], xv[i], v[j]);
         }
-        g0 = wave_sum(g0);
-        u0 = wave_sum(u0);
-        g1 = wave_sum(g1);
-        u1 = wave_sum(u1);
-        if (lane == 0) glu[(long long)p * F + f0] = f32_to_bf16_bits(swiglu<ACT>(g0 + bg0, u0 + bu0));
-        if (lane == 1 && f0 + 1 < F) glu[(long long)p * F + f0 + 1] = f32_to_bf16_bits(swiglu<ACT>(g1 + bg1, u1 + bu1));
+        wave_reduce_groups<2 * R, 2>(v, lane);
+        if (writer) glu[(long long)p * F + f0 + my_r] = f32_to_bf16_bits(swiglu<ACT>(v[0] + bg, v[1] + bu));
     }
 }
 
-// out[t, h] = bf16( sum over pairs (t,k) of w_p * (glu[p] . W2_e[h] + b2_e[h]) ).
-// grid: ceil(H / 4). A workgroup owns 4 output rows for every token; its 4 waves split the
-// distinct experts (wave w takes experts w, w+4, ...), each wave holding the 4 weight rows of an
-// expert in registers and reusing every glu chunk for all 4 rows. Per-wave partial sums meet in
-// LDS and are added in wave order, so the result does not depend on timing.
+// out[t, h] = bf16( sum over valid slots k of w_{t,k} * (glu[t*K+k] . W2_{e}[h] + b2_e[h]) ).
+// grid: ceil(H / 2). Wave w takes the pairs p = w, w+4, ... two at a time (both pairs' weight rows
+// in flight together), accumulating per (token, row) in LDS-free registers of the lane that holds
+// the token; the four waves' partial sums are added in wave order at the end, so the result does
+// not depend on timing.
 template <bool HAS_BIAS, int MAXC>
 __global__ __launch_bounds__(kDecThreads) void moe_decode_down_kernel(
     const uint16_t* __restrict__ glu, const uint16_t* __restrict__ w2, const float* __restrict__ b2,
     const int32_t* __restrict__ idx, const float* __restrict__ route_w, uint16_t* __restrict__ out, int T, int H,
     int F, int E, int K) {
-    __shared__ DecodePlan pl;
-    __shared__ float part[kDecWaves][kDecRowsPerWaveD][kDecMaxTokens];
-    build_plan(pl, idx, T, K, E);
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int h0 = blockIdx.x * kDecRowsPerWaveD;
-    const int nch = F / 8;
-    float acc[kDecRowsPerWaveD];
+    constexpr int HB = kDecDownRows;
+    __shared__ float part[kDecWaves][HB][kDecMaxTokens];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int h0 = blockIdx.x * HB;
+    const int nch = F / 8, P = T * K;
+    float acc[HB];
 #pragma unroll
-    for (int j = 0; j < kDecRowsPerWaveD; ++j) acc[j] = 0.f;  // lane t holds token t's partial sums
+    for (int j = 0; j < HB; ++j) acc[j] = 0.f;  // lane t holds token t's sums
 
-    for (int u = wave; u < pl.U; u += kDecWaves) {
-        const int e = pl.dexp[u], ps = pl.dstart[u], pe = pl.dstart[u + 1];
-        const uint16_t* we = w2 + (long long)e * H * F;
-        u32x4 wr[kDecRowsPerWaveD][MAXC];
+    for (int p0 = wave; p0 < P; p0 += 2 * kDecWaves) {
+        int pp[2], ee[2];
 #pragma unroll
-        for (int j = 0; j < kDecRowsPerWaveD; ++j)
-            load_row<MAXC>(we + (long long)min(h0 + j, H - 1) * F, nch, lane, wr[j]);
-        float bj[kDecRowsPerWaveD];
-#pragma unroll
-        for (int j = 0; j < kDecRowsPerWaveD; ++j) {
-            bj[j] = 0.f;
-            if constexpr (HAS_BIAS) bj[j] = b2[(long long)e * H + min(h0 + j, H - 1)];
+        for (int q = 0; q < 2; ++q) {
+            pp[q] = p0 + q * kDecWaves;
+            const int v = pp[q] < P ? idx[pp[q]] : -1;
+            ee[q] = ((unsigned)v < (unsigned)E) ? v : -1;
         }
-        for (int s = ps; s < pe; ++s) {
-            const int p = pl.spair[s];
-            u32x4 gv[MAXC];
-            load_row<MAXC>(glu + (long long)p * F, nch, lane, gv);
-            float d[kDecRowsPerWaveD];
+        u32x4 wr[2][HB][MAXC], gv[2][MAXC];
 #pragma unroll
-            for (int j = 0; j < kDecRowsPerWaveD; ++j) {
+        for (int q = 0; q < 2; ++q) {
+            if (ee[q] >= 0) {
+                const uint16_t* we = w2 + (long long)ee[q] * H * F;
+#pragma unroll
+                for (int j = 0; j < HB; ++j) load_row<MAXC>(we + (long long)min(h0 + j, H - 1) * F, nch, lane, wr[q][j]);
+                load_row<MAXC>(glu + (long long)pp[q] * F, nch, lane, gv[q]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if (ee[q] < 0) continue;  // wave-uniform
+            float d[HB];
+#pragma unroll
+            for (int j = 0; j < HB; ++j) {
                 d[j] = 0.f;
 #pragma unroll
-                for (int i = 0; i < MAXC; ++i) d[j] = dot8_bf16(wr[j][i], gv[i], d[j]);
+                for (int i = 0; i < MAXC; ++i) d[j] = dot8(wr[q][j][i], gv[q][i], d[j]);
             }
-            const float wp = route_w[p];
-            const int t = p / K;
+            wave_reduce_groups<HB, 1>(d, lane);  // row j's total sits in lanes [j*64/HB, (j+1)*64/HB)
+            const float wp = route_w[pp[q]];
+            const int t = pp[q] / K;
 #pragma unroll
-            for (int j = 0; j < kDecRowsPerWaveD; ++j) {
-                const float v = wave_sum(d[j]);
-                if (lane == t) acc[j] += wp * (v + bj[j]);
+            for (int j = 0; j < HB; ++j) {
+                const float dj = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d[0]), j * (kWave / HB)));
+                float bj = 0.f;
+                if constexpr (HAS_BIAS) bj = b2[(long long)ee[q] * H + min(h0 + j, H - 1)];
+                if (lane == t) acc[j] += wp * (dj + bj);
             }
         }
     }
 #pragma unroll
-    for (int j = 0; j < kDecRowsPerWaveD; ++j) part[wave][j][lane] = acc[j];
+    for (int j = 0; j < HB; ++j) part[wave][j][lane] = acc[j];
     __syncthreads();
-    for (int i = threadIdx.x; i < kDecRowsPerWaveD * T; i += kDecThreads) {
+    for (int i = tid; i < HB * T; i += kDecThreads) {
         const int j = i / T, t = i - j * T, h = h0 + j;
         if (h >= H) continue;
         float sum = 0.f;
@@ -224,18 +253,30 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_down_kernel(
 int decode_max_pairs() { return kDecMaxPairs; }
 int decode_max_tokens() { return kDecMaxTokens; }
 
+template <int ACT, bool HAS_BIAS, int MAXC, int R>
+static void launch_gateup_r(const uint16_t* x, const uint16_t* w1, const float* b1, const int32_t* idx, uint16_t* glu,
+                            int T, int H, int F, int E, int K, hipStream_t s) {
+    dim3 grid(ceil_div(F, kDecWaves * R), min(T * K, E));
+    hipLaunchKernelGGL((moe_decode_gateup_kernel<ACT, HAS_BIAS, MAXC, R>), grid, dim3(kDecThreads), 0, s, x, w1, b1,
+                       idx, glu, T, H, F, E, K);
+}
+
+// R (f per wave): 4 keeps 8 rows in flight per wave, but only if that still leaves about two
+// workgroups per CU when every pair picks a different expert; wide rows (MAXC > 4) use R = 2.
 template <int ACT, bool HAS_BIAS, int MAXC>
 static void launch_gateup_t(const uint16_t* x, const uint16_t* w1, const float* b1, const int32_t* idx, uint16_t* glu,
                             int T, int H, int F, int E, int K, hipStream_t s) {
-    dim3 grid(ceil_div(F, kDecFBlock), T * K);
-    hipLaunchKernelGGL((moe_decode_gateup_kernel<ACT, HAS_BIAS, MAXC>), grid, dim3(kDecThreads), 0, s, x, w1, b1, idx,
-                       glu, T, H, F, E, K);
+    const long long wgs_r4 = (long long)ceil_div(F, kDecWaves * 4) * min(T * K, E);
+    if (MAXC <= 4 && wgs_r4 >= 512)
+        launch_gateup_r<ACT, HAS_BIAS, MAXC, (MAXC <= 4 ? 4 : 2)>(x, w1, b1, idx, glu, T, H, F, E, K, s);
+    else
+        launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, T, H, F, E, K, s);
 }
 
 template <bool HAS_BIAS, int MAXC>
 static void launch_down_t(const uint16_t* glu, const uint16_t* w2, const float* b2, const int32_t* idx,
                           const float* route_w, uint16_t* out, int T, int H, int F, int E, int K, hipStream_t s) {
-    dim3 grid(ceil_div(H, kDecRowsPerWaveD));
+    dim3 grid(ceil_div(H, kDecDownRows));
     hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC>), grid, dim3(kDecThreads), 0, s, glu, w2, b2, idx,
                        route_w, out, T, H, F, E, K);
 }
@@ -270,6 +311,7 @@ hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1,
                          int E, int K, int act, hipStream_t s, hipEvent_t* ev) {
     // ev (optional): 3 events recorded before gate_up, after gate_up, after down.
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
+    if (E > kDecMaxExperts) return hipErrorInvalidValue;
     const int cg = pick_maxc(H), cd = pick_maxc(F);
     mark(0);
     const bool bias = b1 != nullptr;
