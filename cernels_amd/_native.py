@@ -26,6 +26,7 @@ STATUS = {
 }
 LAYOUT_CONCAT, LAYOUT_INTERLEAVED = 0, 1
 ACT_SILU, ACT_GPTOSS = 0, 1
+GATE_UP, DOWN = 0, 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
@@ -45,6 +46,16 @@ _SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P, _P],
     ),
     "cernels_moe_experts_decode_staged": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P, _P],
+    ),
+    "cernels_moe_packed_weight_bytes": (_S, [_I, _I, _I, _I]),
+    "cernels_moe_pack_weights": (ctypes.c_int, [_P, _I, _I, _I, _I, _I, _P, _P]),
+    "cernels_moe_experts_packed": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P],
+    ),
+    "cernels_moe_experts_packed_staged": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P, _P],
     ),

@@ -21,6 +21,13 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
 bool decode_shape_supported(int H, int F);
 int decode_max_pairs();
 int decode_max_tokens();
+size_t packed_weight_bytes(int H, int F, int E, int which);
+hipError_t launch_pack(const uint16_t* src, uint16_t* dst, int E, int H, int F, int layout, int which, hipStream_t s);
+hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1, const void* w2p, const float* b2,
+                                 const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K,
+                                 int bias_interleaved, int act, void* out, int32_t* offsets, int32_t* tile_offsets,
+                                 int32_t* meta, int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts,
+                                 int max_tiles, uint16_t* glu, float* Y, hipStream_t s, hipEvent_t* ev);
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
                          const int32_t* idx, const float* route_w, uint16_t* glu, uint16_t* out, int T, int H, int F,
                          int E, int K, int act, hipStream_t s, hipEvent_t* ev);
@@ -165,6 +172,57 @@ int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* ga
                         size_t workspace_bytes, hipStream_t stream) {
     return cernels_moe_experts_staged(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, T, H, F,
                                       E, K, layout, act, out, workspace, workspace_bytes, stream, nullptr);
+}
+
+// ---- packed weights ------------------------------------------------------------------------------
+
+size_t cernels_moe_packed_weight_bytes(int32_t H, int32_t F, int32_t E, int32_t which) {
+    if (H <= 0 || F <= 0 || E <= 0 || (which != CERNELS_MOE_GATE_UP && which != CERNELS_MOE_DOWN)) return 0;
+    if (H % 64 || F % 64) return 0;
+    return cmoe::packed_weight_bytes(H, F, E, which);
+}
+
+int cernels_moe_pack_weights(const void* src, int32_t H, int32_t F, int32_t E, int32_t layout, int32_t which,
+                             void* dst, hipStream_t stream) {
+    if (!src || !dst || H <= 0 || F <= 0 || E <= 0) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (layout != CERNELS_MOE_LAYOUT_CONCAT && layout != CERNELS_MOE_LAYOUT_INTERLEAVED)
+        return CERNELS_MOE_INVALID_ARGUMENT;
+    if (which != CERNELS_MOE_GATE_UP && which != CERNELS_MOE_DOWN) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (H % 64 || F % 64) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (!aligned16(src) || !aligned16(dst)) return CERNELS_MOE_MISALIGNED;
+    return hip_status(cmoe::launch_pack(static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), E, H, F,
+                                        layout, which, stream));
+}
+
+int cernels_moe_experts_packed_staged(const void* x, const void* gate_up_packed, const float* gate_up_bias,
+                                      const void* down_packed, const float* down_bias, const int32_t* indices,
+                                      const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                                      int32_t bias_layout, int32_t act, void* out, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events) {
+    int st = common_checks(x, gate_up_packed, down_packed, indices, weights, T, H, F, E, K, bias_layout, act, out,
+                           workspace);
+    if (st != CERNELS_MOE_OK || T == 0) return st;
+    if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    const PrefillWs w = prefill_ws(T, H, F, E, K);
+    if (workspace_bytes < w.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
+    char* base = static_cast<char*>(workspace);
+    return hip_status(cmoe::launch_prefill_packed(
+        x, gate_up_packed, gate_up_bias, down_packed, down_bias, indices, weights, T, H, F, E, K,
+        bias_layout == CERNELS_MOE_LAYOUT_INTERLEAVED, act, out, reinterpret_cast<int32_t*>(base + w.offsets),
+        reinterpret_cast<int32_t*>(base + w.tile_offsets), reinterpret_cast<int32_t*>(base + w.meta),
+        reinterpret_cast<int32_t*>(base + w.sorted_pairs), reinterpret_cast<int32_t*>(base + w.tile_expert),
+        reinterpret_cast<int32_t*>(base + w.route_counts), w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
+        reinterpret_cast<float*>(base + w.Y), stream, stage_events));
+}
+
+int cernels_moe_experts_packed(const void* x, const void* gate_up_packed, const float* gate_up_bias,
+                               const void* down_packed, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t bias_layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+    return cernels_moe_experts_packed_staged(x, gate_up_packed, gate_up_bias, down_packed, down_bias, indices,
+                                             weights, T, H, F, E, K, bias_layout, act, out, workspace,
+                                             workspace_bytes, stream, nullptr);
 }
 
 int32_t cernels_moe_decode_max_tokens(void) { return cmoe::decode_max_tokens(); }

@@ -23,6 +23,8 @@ constexpr int kDecMaxPairs = 256;
 constexpr int kDecMaxTokens = 64;
 constexpr int kDecMaxExperts = 1024;  // bitmap of 32 words
 constexpr int kDecDownRows = 2;       // output rows per down workgroup
+constexpr int kDnWaves = 8;           // waves per down workgroup
+constexpr int kDnThreads = kDnWaves * kWave;
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -178,35 +180,37 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
 }
 
 // out[t, h] = bf16( sum over valid slots k of w_{t,k} * (glu[t*K+k] . W2_{e}[h] + b2_e[h]) ).
-// grid: ceil(H / 2). Wave w takes the pairs p = w, w+4, ... two at a time (both pairs' weight rows
-// in flight together), accumulating per (token, row) in LDS-free registers of the lane that holds
-// the token; the four waves' partial sums are added in wave order at the end, so the result does
-// not depend on timing.
-template <bool HAS_BIAS, int MAXC>
-__global__ __launch_bounds__(kDecThreads) void moe_decode_down_kernel(
+// grid: ceil(H / 2), 8 waves. Wave w takes the pairs p = w, w+8, ..., Q at a time (all Q pairs'
+// weight rows and glu rows in flight together), accumulating per (token, row) in the lane that
+// holds the token; the eight waves' partial sums are added in wave order at the end, so the result
+// does not depend on timing. Pair indices are wave-uniform, so expert ids and routing weights come
+// through the scalar cache.
+template <bool HAS_BIAS, int MAXC, int Q>
+__global__ __launch_bounds__(kDnThreads) void moe_decode_down_kernel(
     const uint16_t* __restrict__ glu, const uint16_t* __restrict__ w2, const float* __restrict__ b2,
     const int32_t* __restrict__ idx, const float* __restrict__ route_w, uint16_t* __restrict__ out, int T, int H,
     int F, int E, int K) {
     constexpr int HB = kDecDownRows;
-    __shared__ float part[kDecWaves][HB][kDecMaxTokens];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    __shared__ float part[kDnWaves][HB][kDecMaxTokens];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int h0 = blockIdx.x * HB;
     const int nch = F / 8, P = T * K;
     float acc[HB];
 #pragma unroll
     for (int j = 0; j < HB; ++j) acc[j] = 0.f;  // lane t holds token t's sums
 
-    for (int p0 = wave; p0 < P; p0 += 2 * kDecWaves) {
-        int pp[2], ee[2];
+    for (int p0 = wave; p0 < P; p0 += Q * kDnWaves) {
+        int pp[Q], ee[Q];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            pp[q] = p0 + q * kDecWaves;
+        for (int q = 0; q < Q; ++q) {
+            pp[q] = p0 + q * kDnWaves;
             const int v = pp[q] < P ? idx[pp[q]] : -1;
             ee[q] = ((unsigned)v < (unsigned)E) ? v : -1;
         }
-        u32x4 wr[2][HB][MAXC], gv[2][MAXC];
+        u32x4 wr[Q][HB][MAXC], gv[Q][MAXC];
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < Q; ++q) {
             if (ee[q] >= 0) {
                 const uint16_t* we = w2 + (long long)ee[q] * H * F;
 #pragma unroll
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_down_kernel(
             }
         }
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < Q; ++q) {
             if (ee[q] < 0) continue;  // wave-uniform
             float d[HB];
 #pragma unroll
@@ -240,12 +244,12 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_down_kernel(
 #pragma unroll
     for (int j = 0; j < HB; ++j) part[wave][j][lane] = acc[j];
     __syncthreads();
-    for (int i = tid; i < HB * T; i += kDecThreads) {
+    for (int i = tid; i < HB * T; i += kDnThreads) {
         const int j = i / T, t = i - j * T, h = h0 + j;
         if (h >= H) continue;
         float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) sum += part[w][j][t];
+        for (int w = 0; w < kDnWaves; ++w) sum += part[w][j][t];
         out[(long long)t * H + h] = f32_to_bf16_bits(sum);
     }
 }
@@ -273,11 +277,13 @@ static void launch_gateup_t(const uint16_t* x, const uint16_t* w1, const float* 
         launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, T, H, F, E, K, s);
 }
 
+// Q (pairs in flight per wave) shrinks as rows widen, to bound the registers they take.
 template <bool HAS_BIAS, int MAXC>
 static void launch_down_t(const uint16_t* glu, const uint16_t* w2, const float* b2, const int32_t* idx,
                           const float* route_w, uint16_t* out, int T, int H, int F, int E, int K, hipStream_t s) {
+    constexpr int Q = MAXC <= 2 ? 4 : (MAXC <= 4 ? 2 : 1);
     dim3 grid(ceil_div(H, kDecDownRows));
-    hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC>), grid, dim3(kDecThreads), 0, s, glu, w2, b2, idx,
+    hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, Q>), grid, dim3(kDnThreads), 0, s, glu, w2, b2, idx,
                        route_w, out, T, H, F, E, K);
 }
 

@@ -22,13 +22,12 @@
 // 16-byte chunks XOR-swizzled against LDS bank conflicts (see lds_off).
 // GEMM1's B tile holds 64 gate rows then the 64 matching up rows, so one lane owns the gate and
 // the up value of the same output column and the SwiGLU happens in registers.
-#include "moe_common.h"
+#include "moe_tile.h"
 
 namespace cmoe {
 
 constexpr int kBM = 128;
 constexpr int kBN = 128;  // B-tile rows (GEMM1: 64 gate + 64 up -> 64 glu columns)
-constexpr int kBK = 64;
 constexpr int kGemmThreads = 256;
 constexpr int kTileBytes = kBM * kBK * 2;  // 16 KB, A and B alike
 
@@ -56,14 +55,6 @@ struct GemmParams {
     int ldb;                       // row stride of B (elements)
 };
 
-// LDS tile layout: row-major 128-byte rows (64 bf16 of K) of eight 16-byte chunks; chunk c of row r
-// sits at chunk c ^ ((r >> 1) & 7). gfx950 LDS serves 256 bytes (64 banks) per clock, i.e. 16
-// lanes of a 16-byte read; the swizzle puts the same chunk of any 16 consecutive rows (two rows per
-// 256-byte bank line) on distinct banks, so MFMA fragment reads (consecutive rows, one chunk) are
-// conflict-free.
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * (kBK * 2) + ((chunk ^ swz(row)) << 4); }
-
 __device__ __forceinline__ u32x4 ld_global_16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Transposes 4 K-rows x 8 columns of bf16 (v[i] = row i) into 8 columns x 4 K (two dwords each).
@@ -80,23 +71,6 @@ __device__ __forceinline__ void transpose_4x8(const u32x4 (&v)[4], u32x2 (&o)[8]
             o[j][1] = (a2 & 0xffffu) | (a3 << 16);
         }
     }
-}
-
-// ---- direct global -> LDS copies (gfx950 global_load_lds_dwordx4) ---------------------------------
-// One instruction moves 16 bytes per lane into LDS at M0 + 16*lane (1 KB per wave). The load is
-// issued from inline assembly so the compiler does not wait for every outstanding copy at each
-// barrier; completion is awaited explicitly with s_waitcnt vmcnt(N) before the barrier that
-// publishes a stage.
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const unsigned char*)(p));
-}
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds) : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // ---- concat-layout grouped GEMM: 128 x 256 tiles, 8 waves, 3-stage direct-to-LDS pipeline ------

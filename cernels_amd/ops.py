@@ -106,6 +106,75 @@ def moe_experts(
     return out
 
 
+class PackedExperts:
+    """Expert weights re-laid once in MFMA-fragment order for the packed prefill entry.
+
+    ``gate_up`` / ``down`` hold the packed projections (bf16 tensors with the source element
+    count); biases are kept fp32 in their original column order (``bias_layout``).
+    """
+
+    def __init__(self, gate_up, down, H, F, E, act, bias_layout, gate_up_bias=None, down_bias=None):
+        self.gate_up, self.down = gate_up, down
+        self.H, self.F, self.E = int(H), int(F), int(E)
+        self.act, self.bias_layout = act, bias_layout
+        self.gate_up_bias, self.down_bias = gate_up_bias, down_bias
+
+
+def pack_weights(weight: torch.Tensor, layout: int, which: int, H: int, F: int) -> torch.Tensor:
+    """One projection of every expert, packed by cernels_moe_pack_weights (runs on weight's stream)."""
+    _require(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.dim() == 3,
+             "weight must be a contiguous bf16 CUDA tensor [E, ., .]")
+    E = int(weight.size(0))
+    L = _native.lib()
+    nbytes = L.cernels_moe_packed_weight_bytes(H, F, E, which)
+    _require(nbytes > 0 and nbytes == weight.numel() * 2, f"cannot pack H={H} F={F} (need H % 64 == 0, F % 64 == 0)")
+    out = torch.empty(weight.numel(), dtype=torch.bfloat16, device=weight.device)
+    with torch.cuda.device(weight.device):
+        st = L.cernels_moe_pack_weights(_ptr(weight), H, F, E, layout, which, _ptr(out), _stream(weight.device))
+    check(st, "cernels_moe_pack_weights")
+    return out
+
+
+def pack_experts(gate_up_proj, down_proj, *, layout=LAYOUT_CONCAT, act=ACT_SILU, gate_up_bias=None,
+                 down_bias=None) -> PackedExperts:
+    """Pack both projections (either source layout) for moe_experts_packed."""
+    E = int(gate_up_proj.size(0))
+    if layout == LAYOUT_CONCAT:
+        F, H = int(gate_up_proj.size(1)) // 2, int(gate_up_proj.size(2))
+    else:
+        H, F = int(gate_up_proj.size(1)), int(gate_up_proj.size(2)) // 2
+    gu = pack_weights(gate_up_proj, layout, _native.GATE_UP, H, F)
+    dn = pack_weights(down_proj, layout, _native.DOWN, H, F)
+    f32 = lambda t: None if t is None else t.float().contiguous()  # noqa: E731
+    return PackedExperts(gu, dn, H, F, E, act, layout, f32(gate_up_bias), f32(down_bias))
+
+
+def moe_experts_packed(x: torch.Tensor, packed: PackedExperts, indices: torch.Tensor, weights: torch.Tensor,
+                       topk: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed experts prefill on packed weights (same result contract as moe_experts)."""
+    _require(isinstance(packed, PackedExperts), "packed must come from pack_experts")
+    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2, "x must be bf16 [T, H]")
+    _require(indices.dtype == torch.int32 and indices.is_contiguous(), "indices must be contiguous int32")
+    _require(weights.dtype == torch.float32 and weights.is_contiguous(), "weights must be contiguous float32")
+    T, H = map(int, x.shape)
+    K = int(topk)
+    _require(H == packed.H and tuple(indices.shape) == (T, K) and tuple(weights.shape) == (T, K), "shape mismatch")
+    L = _native.lib()
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
+    if T == 0:
+        return out
+    with torch.cuda.device(x.device):
+        nbytes = L.cernels_moe_experts_workspace_bytes(T, H, packed.F, packed.E, K)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        st = L.cernels_moe_experts_packed(
+            _ptr(x), _ptr(packed.gate_up), _ptr(packed.gate_up_bias), _ptr(packed.down), _ptr(packed.down_bias),
+            _ptr(indices), _ptr(weights), T, H, packed.F, packed.E, K, packed.bias_layout, packed.act, _ptr(out),
+            _ptr(ws), ctypes.c_size_t(nbytes), _stream(x.device))
+    check(st, "cernels_moe_experts_packed")
+    return out
+
+
 def decode_supported(T: int, K: int, H: int, F: int, layout: int = LAYOUT_CONCAT) -> bool:
     """True if the decode entry accepts this shape (otherwise use the prefill entry)."""
     L = _native.lib()
@@ -169,7 +238,7 @@ def gpt_oss_moe_experts(x, gate_up_proj, gate_up_bias, down_proj, down_bias, ind
 
 
 __all__ = [
-    "moe_experts", "route", "decode_supported",
+    "moe_experts", "route", "decode_supported", "PackedExperts", "pack_weights", "pack_experts", "moe_experts_packed",
     "cohere2_moe_experts", "cohere2_moe_experts_decode",
     "deepseek_ocr2_moe_experts", "deepseek_ocr2_moe_experts_decode",
     "qwen3_next_moe_experts", "gpt_oss_moe_experts",

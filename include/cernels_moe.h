@@ -51,6 +51,8 @@ enum cernels_moe_act {
     CERNELS_MOE_ACT_GPTOSS = 1  /* (clamp(up,-7,7) + 1) * g * sigmoid(1.702 g), g = min(gate, 7) */
 };
 
+enum cernels_moe_projection { CERNELS_MOE_GATE_UP = 0, CERNELS_MOE_DOWN = 1 };
+
 const char* cernels_moe_version(void);
 const char* cernels_moe_status_string(int status);
 
@@ -91,6 +93,35 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
                                const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
                                int32_t layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
                                hipStream_t stream, hipEvent_t* stage_events);
+
+/* ---- prefill on packed expert weights ------------------------------------------------------------
+ * The same operation as cernels_moe_experts, on weights re-laid once by cernels_moe_pack_weights
+ * into MFMA-fragment order (each 32x16 operand fragment is 1 KB of contiguous memory in the order
+ * a 64-lane wave reads it). A model packs its expert weights once at load time, as the reference's
+ * gpt-oss loader caches converted copies of its expert tensors (src/kops/registry/gpt_oss_moe_experts.py:14-26);
+ * every later call streams them sequentially. Packing keeps the element count (2FH and HF per
+ * expert) and accepts either source layout; the packed format no longer depends on the source
+ * layout. No counterpart op in the reference: these entries are the fast path behind the same
+ * loaders.
+ *   which: CERNELS_MOE_GATE_UP (src [E,2F,H] concat or [E,H,2F] interleaved) or CERNELS_MOE_DOWN
+ *          (src [E,H,F] concat or [E,F,H] interleaved).
+ *   bias_layout (experts_packed): column order of gate_up_bias, CERNELS_MOE_LAYOUT_CONCAT
+ *          ([gate F | up F]) or CERNELS_MOE_LAYOUT_INTERLEAVED (gate/up alternating).
+ * Limits: H % 64 == 0, F % 64 == 0, E <= 1024. */
+size_t cernels_moe_packed_weight_bytes(int32_t H, int32_t F, int32_t E, int32_t which);
+int cernels_moe_pack_weights(const void* src, int32_t H, int32_t F, int32_t E, int32_t layout, int32_t which,
+                             void* dst, hipStream_t stream);
+int cernels_moe_experts_packed(const void* x, const void* gate_up_packed, const float* gate_up_bias,
+                               const void* down_packed, const float* down_bias, const int32_t* indices,
+                               const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                               int32_t bias_layout, int32_t act, void* out, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+/* With 5 stage events, as cernels_moe_experts_staged. */
+int cernels_moe_experts_packed_staged(const void* x, const void* gate_up_packed, const float* gate_up_bias,
+                                      const void* down_packed, const float* down_bias, const int32_t* indices,
+                                      const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                                      int32_t bias_layout, int32_t act, void* out, void* workspace,
+                                      size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events);
 
 /* ---- decode: fused gather-GEMV over the distinct selected experts -------------------------------
  * Two launches, no atomics on the output, no host sync. Layout CONCAT only.

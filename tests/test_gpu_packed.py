@@ -1,0 +1,139 @@
+"""Packed-weight prefill: the pack kernel's layout, and parity of the packed grouped GEMMs.
+
+The packed layout is this build's own format (MFMA-fragment order), so it is checked against an
+independent numpy construction of the same index map. The packed prefill is then held to the
+same bar as the prefill on the transformers layouts: |out - fp64| <= 2e-2*RMS + half a bf16 ulp,
+the reference's allclose against op_eager, and — at the BASELINE sizes — agreement with the
+unpacked path (same MFMA k-order, so the two agree bit for bit).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN_NAMES, load_golden
+from helpers import assert_reference_verify, assert_within_tolerance, oracle_eager, oracle_fp64, rand_case, run_gpu, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _np_pack(W: np.ndarray, layout: str, which: int, H: int, F: int) -> np.ndarray:
+    """Packed order built group by group: for tile t (4 groups), k-step ks, group w, fragment f,
+    lane l: 8 elements B[16ks + 8(l//32) + j][column of (g, f, l%32)]."""
+    E = W.shape[0]
+    if which == 0:  # B[k][n]: n = gate f or up f
+        Bk = np.transpose(W, (0, 2, 1)) if layout == "concat" else W  # [E, H, 2F] (concat: gate|up; interleaved: g,u,...)
+        if layout == "concat":
+            gate, up = Bk[:, :, :F], Bk[:, :, F:]
+        else:
+            gate, up = Bk[:, :, 0::2], Bk[:, :, 1::2]
+        NG, KS = F // 32, H // 16
+        col = lambda e, g, f, c: (gate if f == 0 else up)[e, :, 32 * g + c]  # noqa: E731
+    else:
+        Bk = np.transpose(W, (0, 2, 1)) if layout == "concat" else W  # [E, F, H]
+        NG, KS = H // 64, F // 16
+        col = lambda e, g, f, c: Bk[e, :, 64 * g + 32 * f + c]  # noqa: E731
+    out = []
+    for e in range(E):
+        for t in range((NG + 3) // 4):
+            groups = list(range(4 * t, min(4 * t + 4, NG)))
+            for ks in range(KS):
+                for g in groups:
+                    for f in range(2):
+                        frag = np.empty((64, 8), dtype=W.dtype)
+                        for lane in range(64):
+                            k0 = 16 * ks + 8 * (lane // 32)
+                            frag[lane] = col(e, g, f, lane % 32)[k0:k0 + 8]
+                        out.append(frag.reshape(-1))
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("layout", ["concat", "interleaved"])
+@pytest.mark.parametrize("which", [0, 1])
+def test_pack_layout(device, layout, which):
+    from cernels_amd import ops
+
+    H, F, E = 192, 320, 2  # 5 gate_up groups / 3 down groups: partial last tiles
+    g = torch.Generator().manual_seed(3)
+    if which == 0:
+        shape = (E, 2 * F, H) if layout == "concat" else (E, H, 2 * F)
+    else:
+        shape = (E, H, F) if layout == "concat" else (E, F, H)
+    W = torch.randint(-30000, 30000, shape, generator=g, dtype=torch.int16)
+    Wd = W.view(torch.bfloat16).contiguous().to(device)
+    lay = ops.LAYOUT_CONCAT if layout == "concat" else ops.LAYOUT_INTERLEAVED
+    got = ops.pack_weights(Wd, lay, which, H, F).view(torch.int16).cpu().numpy()
+    want = _np_pack(W.numpy(), layout, which, H, F)
+    np.testing.assert_array_equal(got, want)
+
+
+def _run_packed(c, device, d=None):
+    from cernels_amd import ops
+
+    d = d or to_device(c, device)
+    layout = ops.LAYOUT_CONCAT if c["layout"] == "concat" else ops.LAYOUT_INTERLEAVED
+    act = ops.ACT_SILU if c["act"] == "silu" else ops.ACT_GPTOSS
+    pk = ops.pack_experts(d["W1"], d["W2"], layout=layout, act=act, gate_up_bias=d["b1"], down_bias=d["b2"])
+    return ops.moe_experts_packed(d["x"], pk, d["idx"], d["w"], d["idx"].shape[1])
+
+
+SMALL = [
+    # (seed, T, H, F, E, K, layout, act, bias, invalid, skew)
+    (0, 37, 128, 64, 8, 3, "concat", "silu", False, 0, 0.0),
+    (1, 300, 256, 192, 16, 4, "concat", "silu", False, 3, 0.0),
+    (2, 513, 64, 128, 5, 2, "concat", "silu", False, 0, 3.0),
+    (3, 100, 192, 128, 4, 2, "interleaved", "gptoss", True, 0, 0.0),
+    (4, 250, 320, 192, 6, 3, "interleaved", "gptoss", True, 2, 0.0),
+    (5, 64, 128, 128, 3, 1, "interleaved", "silu", False, 0, 0.0),
+    (6, 90, 128, 64, 8, 2, "concat", "gptoss", True, 0, 0.0),
+    (7, 1, 128, 64, 16, 8, "concat", "silu", False, 0, 0.0),
+    (8, 1200, 256, 128, 64, 6, "concat", "silu", False, 0, 1.2),
+    (9, 700, 576, 320, 3, 2, "concat", "silu", False, 0, 0.0),  # 9 and 5 groups: idle waves in the last tile
+]
+
+
+@pytest.mark.parametrize("case", SMALL, ids=lambda c: f"T{c[1]}H{c[2]}F{c[3]}E{c[4]}k{c[5]}{c[6]}")
+def test_packed_small(device, case):
+    seed, T, H, Fi, E, K, layout, act, bias, invalid, skew = case
+    c = rand_case(seed, T, H, Fi, E, K, layout=layout, act=act, bias=bias, invalid=invalid, skew=skew,
+                  std=0.05 if act == "gptoss" else 0.02)
+    print(f"[packed small {case}]", flush=True)
+    out = _run_packed(c, device).cpu()
+    assert_within_tolerance(out, oracle_fp64(c), str(case))
+    assert_reference_verify(out, oracle_eager(c), str(case))
+
+
+@pytest.mark.parametrize("name", GOLDEN_NAMES)
+def test_packed_golden(device, name):
+    t, meta = load_golden(name)
+    c = dict(x=t["x"], idx=t["top_k_index"], w=t["top_k_weights"], W1=t["gate_up_proj"], W2=t["down_proj"],
+             b1=t.get("gate_up_proj_bias"), b2=t.get("down_proj_bias"), layout=meta["layout"], act=meta["act"])
+    out = _run_packed(c, device).cpu()
+    assert_reference_verify(out, t["out"], name)
+    assert_within_tolerance(out, oracle_fp64(c), name)
+
+
+@pytest.mark.parametrize("name", ["deepseek_v2_lite_prefill", "a3b_30b_prefill", "gpt_oss_20b_experts", "qwen3_next_zipf"])
+def test_packed_baseline_full_size(device, name):
+    from cernels_amd.configs.registry import BASELINE_SHAPES
+    from cernels_amd.configs.synth import make_inputs, make_weights
+
+    s = BASELINE_SHAPES[name]
+    print(f"[packed full {name}] generating", flush=True)
+    inp, wts = make_inputs(s), make_weights(s)
+    c = dict(x=inp.x, idx=inp.top_k_index, w=inp.top_k_weights, W1=wts.gate_up_proj, W2=wts.down_proj,
+             b1=wts.gate_up_proj_bias, b2=wts.down_proj_bias, layout=s.layout, act=s.act)
+    d = to_device(c, device)
+    print(f"[packed full {name}] run", flush=True)
+    out = _run_packed(c, device, d)
+    out2 = _run_packed(c, device, d)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "not run-to-run deterministic"
+    ref_native = run_gpu(c, device, dev_tensors=d)
+    same = torch.equal(out.view(torch.int16), ref_native.view(torch.int16))
+    rows = torch.randperm(s.tokens, generator=torch.Generator().manual_seed(0))[:48]
+    st = assert_within_tolerance(out.cpu()[rows], oracle_fp64(c, rows), name, strict=True)
+    print(f"[packed full {name}] max|err|/RMS = {st['ratio']:.4f}; bit-identical to unpacked path: {same}", flush=True)
+    assert_reference_verify(out.cpu()[rows], oracle_eager(c, rows), name)
+    assert_within_tolerance(out.cpu(), ref_native.cpu().double(), f"{name} packed vs unpacked")
