@@ -38,19 +38,26 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return __builtin_bit_cast(uint16_t, b);
 }
 
-// SwiGLU variants in fp32.
+// SwiGLU variants in fp32. The logistic factor 1/(1+exp(-x)) uses the hardware reciprocal
+// (v_rcp_f32, about 1 ulp): the result is rounded to bf16 right after, so the division's last bits
+// never reach the output.
 //   silu:   transformers ACT2FN["silu"] = x * sigmoid(x)  (modeling_cohere2_moe.py:131)
 //   gpt-oss: GptOssExperts._apply_gate (modeling_gpt_oss.py:82-88), alpha 1.702, limit 7.0
 template <int ACT>
 __device__ __forceinline__ float swiglu(float gate, float up) {
     if constexpr (ACT == kActSilu) {
-        return gate / (1.0f + __expf(-gate)) * up;
+        return gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate)) * up;
     } else {
         gate = fminf(gate, 7.0f);
         up = fminf(fmaxf(up, -7.0f), 7.0f);
-        float glu = gate / (1.0f + __expf(-1.702f * gate));
+        const float glu = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-1.702f * gate));
         return (up + 1.0f) * glu;
     }
+}
+
+// Two fp32 values -> two round-to-nearest-even bf16 in one dword (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
 }
 
 // Full-wave (64-lane) sum; every lane returns the total.

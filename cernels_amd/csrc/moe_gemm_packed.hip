@@ -2,7 +2,7 @@
 //
 // Same mathematics as the grouped GEMMs on the transformers layouts (moe_gemm.hip):
 //   GEMM1  glu[r, :] = act( X[tok(r), :] · W1_e + b1_e )        SwiGLU / gpt-oss gate in the epilogue
-//   GEMM2  Y[p, :]   = w_p · ( glu[r, :] · W2_e + b2_e )        routing weight in the epilogue
+//   GEMM2  Y[p, :]   = w_p · ( glu[r, :] · W2_e + b2_e )        routing weight in the epilogue (fp32)
 // and the same route kernel, item list and deterministic k-sum combine. What changes is how the
 // weights reach the matrix cores. The weights are re-laid once (cernels_moe_pack_weights) so that
 // each 32x16 MFMA operand fragment is 1 KB of contiguous memory in exactly the order a wave's lanes
@@ -30,6 +30,7 @@ constexpr int kPkBM = 128;
 constexpr int kPkMB = kPkBM / 32;           // 32-row MFMA blocks per item
 constexpr int kPkABytes = kPkBM * kBK * 2;  // 16 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
+constexpr int kPkEpiStride = kPkWaves * 32 + 8;  // bf16 row stride of the GEMM1 output tile in LDS
 
 constexpr int kModePkGateUp = 0;
 constexpr int kModePkDown = 1;
@@ -140,6 +141,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kPkABytes];
     __shared__ int s_pair[kPkBM];
     __shared__ float s_w[kPkBM];
+    __shared__ __attribute__((aligned(16))) uint16_t s_epi[MODE == kModePkGateUp ? kPkBM * kPkEpiStride : 8];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
@@ -269,30 +271,42 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
             default: kloop(IC<4>{}); break;
         }
 
-        // ---- epilogue straight from the accumulators. Element r of a 32x32 block is at row
-        // 8*(r/4) + 4*(lane/32) + (r%4), column lane & 31.
-        if (!active) continue;
+        // ---- epilogue. Element r of a 32x32 accumulator block is at row 8*(r/4) + 4*(lane/32) + (r%4),
+        // column lane & 31.
         if constexpr (MODE == kModePkGateUp) {
-            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            const int fcol = 32 * g + (lane & 31);
-            float bg = 0.f, bu = 0.f;
-            if constexpr (HAS_BIAS) {
-                const float* be = prm.bias + (long long)e * 2 * prm.F;
-                bg = prm.bias_interleaved ? be[2 * fcol] : be[fcol];
-                bu = prm.bias_interleaved ? be[2 * fcol + 1] : be[prm.F + fcol];
-            }
+            // SwiGLU in registers, the bf16 tile staged in LDS, then written as 16-byte chunks: each
+            // output row of the N-tile is one contiguous 512-byte run.
+            if (active) {
+                const int fcol = 32 * g + (lane & 31);
+                float bg = 0.f, bu = 0.f;
+                if constexpr (HAS_BIAS) {
+                    const float* be = prm.bias + (long long)e * 2 * prm.F;
+                    bg = prm.bias_interleaved ? be[2 * fcol] : be[fcol];
+                    bu = prm.bias_interleaved ? be[2 * fcol + 1] : be[prm.F + fcol];
+                }
+                uint16_t* ep = s_epi + wave * 32 + (lane & 31);
 #pragma unroll
-            for (int mb = 0; mb < kPkMB; ++mb) {
-                if (mb >= nmb) break;
+                for (int mb = 0; mb < kPkMB; ++mb) {
+                    if (mb >= nmb) break;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < rows)
-                        glu[(long long)(row_begin + row) * prm.F + fcol] =
-                            f32_to_bf16_bits(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu));
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        ep[row * kPkEpiStride] = f32_to_bf16_bits(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu));
+                    }
                 }
             }
+            __syncthreads();
+            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+            const int col0 = wi.n_idx * kPkWaves * 32;
+            for (int i = tid; i < rows * (kPkWaves * 4); i += kPkThreads) {
+                const int row = i / (kPkWaves * 4), c = i % (kPkWaves * 4);
+                const int col = col0 + 8 * c;
+                if (col < prm.F)
+                    *reinterpret_cast<u32x4*>(glu + (long long)(row_begin + row) * prm.F + col) =
+                        *reinterpret_cast<const u32x4*>(s_epi + row * kPkEpiStride + 8 * c);
+            }
         } else {
+            if (!active) continue;
             float* Y = reinterpret_cast<float*>(prm.out);
             float bn[2] = {0.f, 0.f};
             if constexpr (HAS_BIAS) {
