@@ -152,7 +152,13 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const int it_end = min(total, (xcd + 1) * per);
     const int Kd = prm.Kd, nst = Kd / kBK;
 
-    for (int it = xcd * per + slot; it < it_end; it += slots) {
+    // Items of XCD x are [x*per, x*per + per), handed to its slots in snake order (slot s takes
+    // s, 2*slots-1-s, 2*slots+s, ...) so that long and short items mix on every CU, while the items
+    // that share a weight tile (neighbours in the list) still run at the same time on one XCD.
+    for (int j = 0;; ++j) {
+        const int off = (j & 1) ? (j + 1) * slots - 1 - slot : j * slots + slot;
+        const int it = xcd * per + off;
+        if (off >= per || it >= it_end) break;
         const WorkItem wi = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
         const int e = wi.e, row_begin = wi.row_begin, rows = wi.rows;
         const int g = wi.n_idx * kPkWaves + wave;
@@ -195,9 +201,9 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         // Activation chunks in a two-slot register ring (loaded two stages before their MFMAs,
         // written to LDS one stage before); weight fragments in one slot per k-step, refilled with the
         // next stage's k-step as soon as its MFMAs have read it (one stage ahead). Every load is visible to the compiler, which waits for exactly the loads each
-        // use needs. The step sequence has no data-dependent branches, so those waits stay exact:
-        // past the last stage a step re-reads the last stage (an L2 hit), and a wave whose column
-        // group is past the end computes on valid fragments of the tile and stores nothing.
+        // use needs. Loads are never behind a branch, so those waits stay exact: past the last stage
+        // a step re-reads the last stage (an L2 hit), and a wave whose column group is past the end
+        // loads valid fragments of the tile, skips its MFMAs and stores nothing.
         u32x4 aring[2][2];
         u32x4 breg[4][2];  // k-step q of the current stage, refilled with k-step q of the next
         auto load_a = [&](int s, auto rc) {
@@ -243,8 +249,10 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     const bf16x8 b1 = __builtin_bit_cast(bf16x8, breg[q][1]);
 #pragma unroll
                     for (int mb = 0; mb < NMB; ++mb) {
-                        acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], b0, acc[mb][0], 0, 0, 0);
-                        acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], b1, acc[mb][1], 0, 0, 0);
+                        if (active) {  // wave-uniform, no loads inside: the compiler's waits stay exact
+                            acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], b0, acc[mb][0], 0, 0, 0);
+                            acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], b1, acc[mb][1], 0, 0, 0);
+                        }
                         if (q + 1 < 4) af[mb] = read_af(q + 1, mb);
                     }
                     load_b(s + 1, q);  // k-step q of the next stage into the registers just consumed
