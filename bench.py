@@ -7,6 +7,12 @@ through the C ABI with preallocated output and workspace. The headline is BASELI
 configs[1] (``deepseek_v2_lite_prefill``: T=2048, H=1280, F=896, E=64, top-6); the other
 BASELINE workloads are measured the same way and reported under ``per_config``.
 
+Prefill runs on expert weights packed once in MFMA-fragment order (``cernels_moe_pack_weights``,
+what the drop-in loaders cache on a module at first use); the pack itself is outside the timed
+region and reported as ``pack_ms``. The same workload on the weights as stored (transformers
+layout, ``cernels_moe_experts``) is timed beside it as ``native_layout``. Decode streams the
+weights as stored.
+
 Timing: W untimed warmup steps, then exactly K steps between two ``torch.cuda.synchronize()``;
 the step time is the HIP-event time of the K steps / K. Each step also records HIP events between
 its kernels on the launch stream, which gives each kernel's average duration (``stages``).
@@ -15,19 +21,26 @@ rotation exceed 1 GiB (4x the 256 MB Infinity Cache).
 
 ``roofline`` describes the dominant kernel of the headline: algorithmic bytes (or FLOPs) of one
 launch / its average duration, against MI355X's 8 TB/s HBM or 2.5 PFLOP/s dense bf16 MFMA peak,
-whichever bounds that kernel at its arithmetic intensity. ``cpu_baseline`` times the op_eager
-restatement (the reference's baseline) on the host CPU on the same inputs.
+whichever bounds that kernel at its arithmetic intensity. ``roofline.traffic`` is that kernel's
+measured HBM bytes per launch: two child runs of this script under ``rocprofv3 --pmc FETCH_SIZE``
+and ``--pmc WRITE_SIZE``, each counter scaled by what it reads for a 256 MiB device copy (started
+before this process touches the GPU; skipped with --no-traffic). ``cpu_baseline`` times the
+op_eager restatement (the reference's baseline) on the host CPU on the same inputs.
 """
 
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes
 import json
 import math
 import os
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -39,6 +52,12 @@ MFMA_BF16_PEAK_TFS = 2500.0
 RIDGE = MFMA_BF16_PEAK_TFS * 1e12 / (HBM_PEAK_GBS * 1e9)  # FLOP/byte
 METRIC = "MoE experts prefill TFLOP/s + decode HBM GB/s (% roofline), 1 MI355X"
 COLD_BYTES = 1 << 30
+CAL_MIB = 256
+# kernel-name fragments of each stage's kernels in a rocprofv3 trace
+KERNEL_OF_STAGE = {
+    "packed": {"gate_up": "moe_gemm_packed_kernel<0", "down": "moe_gemm_packed_kernel<1"},
+    "native": {"gate_up": "moe_gemm_v3_kernel<0", "down": "moe_gemm_v3_kernel<1"},
+}
 
 
 def _hip():
@@ -74,11 +93,11 @@ def stage_model(shape, U, P, stage):
     T, H, F, E = shape.tokens, shape.hidden, shape.ffn, shape.experts
     if stage == "route":
         return 0.0, P * 4 * 2 + (E + 1) * 8
-    if stage == "gate_up":
-        w = U * 2 * F * H * 2 + (U * 2 * F * 2 if shape.bias else 0)
+    if stage == "gate_up":  # weights + fp32 bias, x read, glu bf16 written, pair ids + weights
+        w = U * 2 * F * H * 2 + (U * 2 * F * 4 if shape.bias else 0)
         return 2.0 * P * H * 2 * F, w + T * H * 2 + P * F * 2 + P * 8
-    if stage == "down":
-        w = U * H * F * 2 + (U * H * 2 if shape.bias else 0)
+    if stage == "down":  # weights + fp32 bias, glu read, fp32 weighted rows written
+        w = U * H * F * 2 + (U * H * 4 if shape.bias else 0)
         return 2.0 * P * F * H, w + P * F * 2 + P * H * 4 + P * 8
     if stage == "combine":
         return float(P * H), P * H * 4 + T * H * 2 + P * 4
@@ -99,7 +118,33 @@ def roofline_of(flops, nbytes, ms):
     return dict(bound="hbm", achieved=ach, peak=HBM_PEAK_GBS, unit="GB/s", frac=ach / HBM_PEAK_GBS, intensity=ai)
 
 
-def run_config(shape, steps, warmup, dev, hip, log):
+def _timed_steps(step, stages, steps, warmup, hip, stream):
+    """Runs warmup + timed steps; returns (ms per step, wall ms per step, {stage: mean ms})."""
+    import torch
+
+    for i in range(warmup):
+        step(i, None)
+    torch.cuda.synchronize()
+    nst = len(stages) + 1
+    ev = Events(hip, nst * steps + 2)
+    arrs_keep = [(ctypes.c_void_p * nst)(*ev.ev[2 + s * nst: 2 + (s + 1) * nst]) for s in range(steps)]
+    arrs = [ctypes.cast(a, ctypes.c_void_p) for a in arrs_keep]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    hip.hipEventRecord(ev.ev[0], ctypes.c_void_p(stream))
+    for s in range(steps):
+        step(s, arrs[s])
+    hip.hipEventRecord(ev.ev[1], ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - wall0) * 1e3 / steps
+    ms = ev.ms(0, 1) / steps
+    stage_ms = {name: statistics.mean(ev.ms(2 + s * nst + j, 2 + s * nst + j + 1) for s in range(steps))
+                for j, name in enumerate(stages)}
+    ev.close()
+    return ms, wall, stage_ms
+
+
+def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
     import torch
 
     from cernels_amd import _native
@@ -127,48 +172,70 @@ def run_config(shape, steps, warmup, dev, hip, log):
     T, H, F, E, K = shape.tokens, shape.hidden, shape.ffn, shape.experts, shape.top_k
     layout = _native.LAYOUT_INTERLEAVED if shape.layout == "interleaved" else _native.LAYOUT_CONCAT
     act = _native.ACT_GPTOSS if shape.act == "gptoss" else _native.ACT_SILU
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    paths = {}
+
     if shape.decode:
         nbytes = L.cernels_moe_experts_decode_workspace_bytes(T, H, F, E, K)
-        fn, stages = L.cernels_moe_experts_decode_staged, ["decode_gate_up", "decode_down"]
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+        def step(i, ev_arr):
+            st = L.cernels_moe_experts_decode_staged(ptr(x), ptr(W1[i % copies]), ptr(b1), ptr(W2[i % copies]),
+                                                     ptr(b2), ptr(idx), ptr(rw), T, H, F, E, K, layout, act, ptr(out),
+                                                     ptr(ws), ctypes.c_size_t(nbytes), stream, ev_arr)
+            _native.check(st, shape.name)
+
+        paths["decode"] = _timed_steps(step, ["decode_gate_up", "decode_down"], steps, warmup, hip, stream)
+        main_path = "decode"
+        pack_ms = None
     else:
         nbytes = L.cernels_moe_experts_workspace_bytes(T, H, F, E, K)
-        fn, stages = L.cernels_moe_experts_staged, ["route", "gate_up", "down", "combine"]
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
-    nst = len(stages) + 1
-    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        stages = ["route", "gate_up", "down", "combine"]
+        # one-time packing of every weight copy (timed on its own, outside the steps)
+        pk = []
+        ev = Events(hip, 2)
+        hip.hipEventRecord(ev.ev[0], ctypes.c_void_p(stream))
+        for c in range(copies):
+            p1 = torch.empty_like(W1[c])
+            p2 = torch.empty_like(W2[c])
+            _native.check(L.cernels_moe_pack_weights(ptr(W1[c]), H, F, E, layout, _native.GATE_UP, ptr(p1), stream),
+                          "pack gate_up")
+            _native.check(L.cernels_moe_pack_weights(ptr(W2[c]), H, F, E, layout, _native.DOWN, ptr(p2), stream),
+                          "pack down")
+            pk.append((p1, p2))
+        hip.hipEventRecord(ev.ev[1], ctypes.c_void_p(stream))
+        torch.cuda.synchronize()
+        pack_ms = ev.ms(0, 1) / copies
+        ev.close()
 
-    def step(i, ev_arr):
-        st = fn(ptr(x), ptr(W1[i % copies]), ptr(b1), ptr(W2[i % copies]), ptr(b2), ptr(idx), ptr(rw), T, H, F, E,
-                K, layout, act, ptr(out), ptr(ws), ctypes.c_size_t(nbytes), stream, ev_arr)
-        _native.check(st, shape.name)
+        def step_packed(i, ev_arr):
+            p1, p2 = pk[i % copies]
+            st = L.cernels_moe_experts_packed_staged(ptr(x), ptr(p1), ptr(b1), ptr(p2), ptr(b2), ptr(idx), ptr(rw), T, H,
+                                                     F, E, K, layout, act, ptr(out), ptr(ws), ctypes.c_size_t(nbytes),
+                                                     stream, ev_arr)
+            _native.check(st, shape.name)
 
-    for i in range(warmup):
-        step(i, None)
-    torch.cuda.synchronize()
-    ev = Events(hip, nst * steps + 2)
-    arrs_keep = [(ctypes.c_void_p * nst)(*ev.ev[2 + s * nst: 2 + (s + 1) * nst]) for s in range(steps)]
-    arrs = [ctypes.cast(a, ctypes.c_void_p) for a in arrs_keep]
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    hip.hipEventRecord(ev.ev[0], ctypes.c_void_p(stream))
-    for s in range(steps):
-        step(s, arrs[s])
-    hip.hipEventRecord(ev.ev[1], ctypes.c_void_p(stream))
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - wall0) * 1e3 / steps
-    ms = ev.ms(0, 1) / steps
-    stage_ms = {}
-    for j, name in enumerate(stages):
-        vals = [ev.ms(2 + s * nst + j, 2 + s * nst + j + 1) for s in range(steps)]
-        stage_ms[name] = statistics.mean(vals)
-    ev.close()
+        paths["packed"] = _timed_steps(step_packed, stages, steps, warmup, hip, stream)
+        main_path = "packed"
+        del pk
+        if with_native:
+            def step_native(i, ev_arr):
+                st = L.cernels_moe_experts_staged(ptr(x), ptr(W1[i % copies]), ptr(b1), ptr(W2[i % copies]), ptr(b2),
+                                                  ptr(idx), ptr(rw), T, H, F, E, K, layout, act, ptr(out), ptr(ws),
+                                                  ctypes.c_size_t(nbytes), stream, ev_arr)
+                _native.check(st, shape.name)
+
+            paths["native"] = _timed_steps(step_native, stages, steps, warmup, hip, stream)
+
+    ms, wall, stage_ms = paths[main_path]
     flops = shape.flops()
     alg_bytes = touched + 2 * T * H * 2 + P * 8
     t_roof_ms = max(flops / (MFMA_BF16_PEAK_TFS * 1e12), alg_bytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     rec = dict(
-        workload=shape.name, decode=shape.decode, tokens=T, hidden=H, ffn=F, experts=E, top_k=K,
+        workload=shape.name, decode=shape.decode, path=main_path, tokens=T, hidden=H, ffn=F, experts=E, top_k=K,
         distinct_experts=U, weight_copies=copies, ms=ms, wall_ms_per_step=wall,
         tflops=flops / (ms * 1e-3) / 1e12, gbs=alg_bytes / (ms * 1e-3) / 1e9,
         mfma_peak_frac=flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS,
@@ -176,12 +243,19 @@ def run_config(shape, steps, warmup, dev, hip, log):
         attainable_frac=t_roof_ms / ms, algorithmic_bytes=alg_bytes, flops=flops,
         stages={k: dict(ms=v, **roofline_of(*stage_model(shape, U, P, k), v)) for k, v in stage_ms.items()},
     )
-    log(f"[{shape.name}] {ms:.4f} ms/step  {rec['tflops']:.1f} TFLOP/s  {rec['gbs']:.0f} GB/s  "
+    if pack_ms is not None:
+        rec["pack_ms"] = pack_ms
+    if "native" in paths:
+        nms, _, nst = paths["native"]
+        rec["native_layout"] = dict(ms=nms, tflops=flops / (nms * 1e-3) / 1e12, stages_ms=nst)
+    log(f"[{shape.name}] {main_path}: {ms:.4f} ms/step  {rec['tflops']:.1f} TFLOP/s  {rec['gbs']:.0f} GB/s  "
         f"attainable {rec['attainable_frac'] * 100:.1f}%  stages " +
-        " ".join(f"{k}={v['ms'] * 1e3:.1f}us" for k, v in rec["stages"].items()))
+        " ".join(f"{k}={v['ms'] * 1e3:.1f}us" for k, v in rec["stages"].items()) +
+        (f"  | native layout {rec['native_layout']['ms'] * 1e3:.1f}us" if "native_layout" in rec else "") +
+        (f"  | pack {pack_ms:.2f} ms once" if pack_ms is not None else ""))
     del W1, W2, ws, out
     torch.cuda.empty_cache()
-    return rec, (inp, shape)
+    return rec
 
 
 def cpu_baseline(shape, budget_s, log):
@@ -223,6 +297,67 @@ def cpu_baseline(shape, budget_s, log):
     )
 
 
+# ---- HBM traffic per launch (rocprofv3 counters, child processes) ----------------------------------
+
+def _inner_traffic(headline):
+    """Child mode: a 256 MiB calibration copy, then a few packed steps of the headline workload."""
+    import torch
+
+    from cernels_amd.configs.registry import BASELINE_SHAPES
+
+    dev = torch.device("cuda:0")
+    n = CAL_MIB << 20
+    src = torch.ones(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)  # the first copyBuffer dispatch of this process: the calibration copy
+    torch.cuda.synchronize()
+    del src, dst
+    run_config(BASELINE_SHAPES[headline], 5, 2, dev, _hip(), lambda m: None, with_native=False)
+
+
+def _counter_rows(path):
+    with open(path) as f:
+        return list(csv.DictReader(f))
+
+
+def measure_traffic(headline, log, timeout_s=180):
+    """Per-launch HBM MB of the headline's packed kernels from FETCH_SIZE / WRITE_SIZE passes."""
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return None, "rocprofv3 not found"
+    res = {}
+    with tempfile.TemporaryDirectory(prefix="bench_pmc_") as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            out = Path(tmp) / counter
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", str(out), "-o", "c", "--",
+                   sys.executable, str(Path(__file__).resolve()), "--inner-traffic", headline]
+            try:
+                r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s, cwd=tmp,
+                                   env=dict(os.environ, TMPDIR=tmp), start_new_session=True)
+            except subprocess.TimeoutExpired:
+                return None, f"rocprofv3 --pmc {counter} timed out"
+            files = list(out.rglob("*counter_collection.csv"))
+            if not files:
+                return None, f"rocprofv3 --pmc {counter} wrote no counters (rc={r.returncode})"
+            rows = _counter_rows(files[0])
+            rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+            cal = next((float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]), None)
+            if not cal:
+                return None, "calibration copy not found in the trace"
+            scale = (CAL_MIB * 1024) / cal  # true KiB per counted KiB
+            per = {}
+            for stage, frag in KERNEL_OF_STAGE["packed"].items():
+                vals = [float(r["Counter_Value"]) for r in rows if frag in r["Kernel_Name"]]
+                if vals:
+                    per[stage] = statistics.mean(vals) * scale * 1024 / 1e6  # MB per launch
+            res[counter] = dict(scale=scale, per_stage_mb=per)
+    log(f"[traffic] FETCH scale {res['FETCH_SIZE']['scale']:.3f}, WRITE scale {res['WRITE_SIZE']['scale']:.3f}; "
+        + ", ".join(f"{k} {res['FETCH_SIZE']['per_stage_mb'].get(k, 0) + res['WRITE_SIZE']['per_stage_mb'].get(k, 0):.1f} MB"
+                    for k in KERNEL_OF_STAGE["packed"]))
+    return res, None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -231,35 +366,33 @@ def main():
     ap.add_argument("--configs", default="all", help="'all', 'headline' or a comma list of BASELINE workload names")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-native", action="store_true", help="skip timing prefill on the weights as stored")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE child runs")
+    ap.add_argument("--inner-traffic", metavar="WORKLOAD", help=argparse.SUPPRESS)
     ap.add_argument("--report", default=str(ROOT / "gpurun_out" / "bench_report.json"))
-    ap.add_argument("--copy-calibration-mib", type=int, default=0,
-                    help="also run a plain device copy of this many MiB (a known-size kernel against which "
-                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings are scaled)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the experts op on one GPU "
               f"(the multi-GPU design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-
-    import torch
+    if args.inner_traffic:
+        _inner_traffic(args.inner_traffic)
+        return
 
     from cernels_amd.configs.registry import BASELINE_ORDER, BASELINE_SHAPES, HEADLINE
 
     log = lambda m: print(m, file=sys.stderr, flush=True)  # noqa: E731
+    traffic, traffic_note = (None, "skipped (--no-traffic)")
+    if not args.no_traffic:  # child processes first, before this process initialises the GPU
+        traffic, traffic_note = measure_traffic(HEADLINE, log)
+
+    import torch
+
     if not torch.cuda.is_available():
         log("bench.py: no GPU visible")
         sys.exit(1)
     dev = torch.device("cuda:0")
     hip = _hip()
-    if args.copy_calibration_mib > 0:
-        n = args.copy_calibration_mib << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[copy calibration] copied {args.copy_calibration_mib} MiB")
-        del src, dst
     if args.configs == "all":
         names = [HEADLINE] + [n for n in BASELINE_ORDER if n != HEADLINE]
     elif args.configs == "headline":
@@ -268,13 +401,22 @@ def main():
         names = [n.strip() for n in args.configs.split(",") if n.strip()]
     per = {}
     for n in names:
-        rec, _ = run_config(BASELINE_SHAPES[n], args.steps, args.warmup, dev, hip, log)
-        per[n] = rec
+        per[n] = run_config(BASELINE_SHAPES[n], args.steps, args.warmup, dev, hip, log, with_native=not args.no_native)
     head = per.get(HEADLINE) or per[names[0]]
     dom_name, dom = max(head["stages"].items(), key=lambda kv: kv[1]["ms"])
+    traffic_mb = None
+    if traffic and head["path"] == "packed" and dom_name in traffic["FETCH_SIZE"]["per_stage_mb"]:
+        traffic_mb = traffic["FETCH_SIZE"]["per_stage_mb"][dom_name] + traffic["WRITE_SIZE"]["per_stage_mb"].get(dom_name, 0.0)
     roofline = dict(bound=dom["bound"], achieved=round(dom["achieved"], 3), peak=dom["peak"], unit=dom["unit"],
-                    frac=round(dom["frac"], 5), traffic=None, kernel=dom_name, kernel_ms=round(dom["ms"], 5),
+                    frac=round(dom["frac"], 5),
+                    traffic=None if traffic_mb is None else round(traffic_mb * 1e6),
+                    traffic_unit="bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
+                    kernel=dom_name, kernel_ms=round(dom["ms"], 5),
+                    algorithmic_bytes=round(stage_model(BASELINE_SHAPES[head["workload"]], head["distinct_experts"],
+                                                        BASELINE_SHAPES[head["workload"]].pairs, dom_name)[1]),
                     intensity_flop_per_byte=round(dom["intensity"], 2))
+    if traffic_mb is None:
+        roofline["traffic_note"] = traffic_note or "dominant kernel not in the counter trace"
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(BASELINE_SHAPES[head["workload"]], args.cpu_seconds, log)
@@ -294,19 +436,23 @@ def main():
         "data": "synthetic (seeded CPU-generated bf16 x ~ N(0,1), weights ~ N(0,0.02), softmax top-k routing)",
         "config": {"workload": head["workload"], "tokens": head["tokens"], "hidden": head["hidden"],
                    "ffn": head["ffn"], "experts": head["experts"], "top_k": head["top_k"],
+                   "weights": "packed once (MFMA-fragment order), pack time excluded" if head["path"] == "packed"
+                   else "as stored",
                    "mfma_peak_frac": round(head["mfma_peak_frac"], 5),
                    "attainable_roofline_frac": round(head["attainable_frac"], 5)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "per_config": {
-            n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items() if k != "stages"}
+            n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items() if k not in ("stages", "native_layout")}
             | {"stages_ms": {s: round(v["ms"], 5) for s, v in r["stages"].items()}}
+            | ({"native_layout_ms": round(r["native_layout"]["ms"], 5)} if "native_layout" in r else {})
             for n, r in per.items()
         },
     }
     try:
         Path(args.report).parent.mkdir(parents=True, exist_ok=True)
-        Path(args.report).write_text(json.dumps({"line": line, "per_config_full": per}, indent=1, default=float))
+        Path(args.report).write_text(json.dumps({"line": line, "per_config_full": per, "traffic": traffic}, indent=1,
+                                                default=float))
     except OSError:
         pass
     print(json.dumps(line), flush=True)

@@ -2,28 +2,22 @@
 
 The router (linear + top-k + softmax) runs here, in the timed path; only the hidden state and
 the ``GptOssMLP``-shaped module come from the caller. The native op does the routing, both
-grouped GEMMs with biases and the clamped SwiGLU. Layout: ``gate_up_proj[e]`` is [H, 2F] with
-interleaved gate/up columns, ``down_proj[e]`` is [F, H].
+grouped GEMMs with biases and the clamped SwiGLU, on a packed copy of the expert weights made on
+first use and cached on the module. Layout: ``gate_up_proj[e]`` is [H, 2F] with interleaved
+gate/up columns, ``down_proj[e]`` is [F, H].
 """
 
 import torch
 
+from cernels_amd import ops
 from cernels_amd.kops.registry._local import load
+from cernels_amd.kops.registry._packed import packed_experts
 
 
 def _weights(e):
-    # Expert weights + fp32 bias casts, done once per module (the op consumes fp32 biases and
-    # these tensors never change), as the reference caches them (:14-26).
-    w = getattr(e, "_kops_weights", None)
-    if w is None:
-        w = (
-            e.gate_up_proj.data.contiguous(),
-            e.gate_up_proj_bias.data.float().contiguous(),
-            e.down_proj.data.contiguous(),
-            e.down_proj_bias.data.float().contiguous(),
-        )
-        e._kops_weights = w
-    return w
+    # Expert weights packed once per module with fp32 bias copies (the op consumes fp32 biases and
+    # these tensors never change), as the reference caches its converted copies (:14-26).
+    return packed_experts(e, layout=ops.LAYOUT_INTERLEAVED, act=ops.ACT_GPTOSS, with_bias=True)
 
 
 def kernel(x, mlp):
@@ -33,13 +27,10 @@ def kernel(x, mlp):
     xf = x.reshape(-1, hidden).contiguous()
     with torch.no_grad():
         _logits, scores, indices = mlp.router(xf)  # timed router (same code as the baseline)
-        gate_up, gate_up_bias, down, down_bias = _weights(mlp.experts)
-        out = load("gpt_oss_moe_experts").gpt_oss_moe_experts(
+        load("gpt_oss_moe_experts")  # fail loudly if the native library is missing
+        out = ops.moe_experts_packed(
             xf,
-            gate_up,
-            gate_up_bias,
-            down,
-            down_bias,
+            _weights(mlp.experts),
             indices.to(torch.int32).contiguous(),
             scores.float().contiguous(),
             mlp.router.top_k,
