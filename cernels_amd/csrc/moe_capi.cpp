@@ -4,6 +4,8 @@
 
 #include <cstdint>
 
+#include <algorithm>
+
 #include "../../include/cernels_moe.h"
 
 namespace cmoe {
@@ -13,6 +15,7 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
                         hipStream_t stream);
 size_t route_workspace_bytes(int T, int K, int E);
 int gemm_tile_m();
+int packed_tile_m();
 hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
@@ -49,7 +52,7 @@ struct PrefillWs {
 PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     PrefillWs w{};
     const long long P = (long long)T * K;
-    const int bm = cmoe::gemm_tile_m();
+    const int bm = std::min(cmoe::gemm_tile_m(), cmoe::packed_tile_m());  // M-tile list sized for either GEMM
     w.capacity = (int)((P + bm - 1) / bm + (P < E ? P : E));
     size_t o = 0;
     w.offsets = o;      o = align_up(o + sizeof(int32_t) * (E + 1));

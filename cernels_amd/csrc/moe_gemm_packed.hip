@@ -6,72 +6,77 @@
 // and the same route kernel, item list and deterministic k-sum combine. What changes is how the
 // weights reach the matrix cores. The weights are re-laid once (cernels_moe_pack_weights) so that
 // each 32x16 MFMA operand fragment is 1 KB of contiguous memory in exactly the order a wave's lanes
-// consume it. A wave then streams its weight columns straight into registers with one contiguous
-// 1 KB read per fragment: every HBM request is a full, sequential line run, nothing of the weights
-// goes through LDS, and how many bytes are in flight is bounded by registers rather than by LDS.
-// Only the activation tile (token rows gathered through the expert-sorted pair list) is staged in
-// LDS, since all four waves of a workgroup share it.
+// consume it. A wave streams its weight columns straight into registers with one contiguous 1 KB
+// read per fragment: nothing of the weights goes through LDS. Only the activation tile (token rows
+// gathered through the expert-sorted pair list) is staged in LDS, where all eight waves of the
+// workgroup read it.
 //
-// Workgroup: 8 waves, two per SIMD, one workgroup per CU. Each wave owns one 64-column group of the
-// N-tile (GEMM1: 32 gate + the 32 matching up columns; GEMM2: 64 output columns) for all 128 rows of
-// the item, so every weight fragment is loaded once per workgroup and used by 4 MFMAs. All waves
-// skip the item's empty 32-row blocks, so an item of fewer than 128 rows costs MFMA time in
-// proportion to its rows. K advances in stages of 64: weight loads are issued one stage,
-// activation loads two stages before their MFMAs.
+// Workgroup: 8 waves (two per SIMD), one workgroup per CU, items of 256 rows x 8 fragments. Each
+// wave owns one 32-column weight fragment for all 256 rows of the item (eight 32x32 accumulator
+// blocks), so a weight fragment is fetched once per item and feeds 8 MFMAs, and the activation tile
+// is fetched once per item and feeds 8 fragments. The CU's vector-memory pipe (address and data
+// units, L1) carries 8 KB per 32 MFMAs of a wave, which is what bounds this kernel at these shapes,
+// not HBM. Blocks past the item's rows are skipped (the k-loop is instantiated per block count).
+// K advances in stages of 64: weight loads are issued two stages, activation loads one stage
+// before their MFMAs.
+//
+// GEMM1 fragments hold 16 gate and the 16 matching up columns, so one wave holds both inputs of the
+// gated activation for its 16 glu columns; a v_permlane16_swap pairs them up in the epilogue.
 #include <type_traits>
 
 #include "moe_tile.h"
 
 namespace cmoe {
 
-constexpr int kPkWaves = 8;                 // waves per workgroup = column groups per N-tile
+constexpr int kPkWaves = 8;                 // waves per workgroup = fragments per N-tile
 constexpr int kPkThreads = kPkWaves * kWave;
-constexpr int kPkBM = 128;
+constexpr int kPkBM = 256;
 constexpr int kPkMB = kPkBM / 32;           // 32-row MFMA blocks per item
-constexpr int kPkABytes = kPkBM * kBK * 2;  // 16 KB A stage
+constexpr int kPkABytes = kPkBM * kBK * 2;  // 32 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
-constexpr int kPkEpiStride = kPkWaves * 32 + 8;  // bf16 row stride of the GEMM1 output tile in LDS
+constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
+constexpr int kPkEpiStride = kPkGlu + 8;    // bf16 row stride of the GEMM1 output tile in LDS
+constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
 
 constexpr int kModePkGateUp = 0;
 constexpr int kModePkDown = 1;
 
-// Packed layout of one projection, viewed as B[k][n] (reduction length Kd, KS = Kd/16 k-steps) with
-// NG column groups of two 32-column fragments:
-//   gate_up: group g = glu columns [32g, 32g+32); fragment 0 = gate, 1 = up.  Kd = H, NG = F/32.
-//   down:    group g = output columns [64g, 64g+64); fragment f = [64g+32f, +32). Kd = F, NG = H/64.
-// Groups are bundled by four (an N-tile: one group per wave) and stored k-step-major inside a tile, so
-// the four waves of a workgroup read one contiguous 8 KB run per k-step. Lane l of fragment
-// (g, ks, f) holds B[16ks + 8(l/32) + j][column l%32 of the fragment], j = 0..7.
+// Packed layout of one projection, viewed as B[k][n] (reduction length Kd, KS = Kd/16 k-steps) cut
+// into NF fragments of 32 columns:
+//   gate_up: fragment c = gate columns [16c, 16c+16) then up columns [16c, 16c+16). Kd = H, NF = F/16.
+//   down:    fragment c = output columns [32c, 32c+32).                           Kd = F, NF = H/32.
+// Fragments are bundled by eight (an N-tile: one fragment per wave) and stored k-step-major inside a
+// tile, so the eight waves of a workgroup read one contiguous 8 KB run per k-step. Lane l of
+// fragment (c, ks) holds B[16ks + 8(l/32) + j][column l%32 of the fragment], j = 0..7.
 // Returns the fragment's index in 1 KB units.
-__host__ __device__ inline long long packed_frag(int e, int g, int ks, int f, int NG, int KS) {
-    const int t = g >> 2, w = g & 3, nw = min(4, NG - 4 * t);
-    return ((long long)e * NG * KS + 4LL * KS * t + (long long)ks * nw + w) * 2 + f;
+__host__ __device__ inline long long packed_frag(int e, int c, int ks, int NF, int KS) {
+    const int t = c >> 3, w = c & 7, nw = min(8, NF - 8 * t);
+    return (long long)e * NF * KS + 8LL * KS * t + (long long)ks * nw + w;
 }
 
 // ---- packing (one-time, per weight tensor) ---------------------------------------------------------
-// One thread per 16-byte lane chunk of the packed output, in logical (e, g, ks, f, lane) order.
+// One thread per 16-byte lane chunk of the packed output, in logical (e, c, ks, lane) order.
 template <int WHICH, int LAYOUT>
 __global__ __launch_bounds__(256) void moe_pack_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                        int E, int H, int F) {
     const int Kd = WHICH == 0 ? H : F;
-    const int NG = WHICH == 0 ? F / 32 : H / 64;
+    const int NF = WHICH == 0 ? F / 16 : H / 32;
     const int KS = Kd / 16;
-    const long long total = (long long)E * NG * KS * 2 * kWave;
+    const long long total = (long long)E * NF * KS * kWave;
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
     const int lane = (int)(i % kWave);
     long long q = i / kWave;
-    const int f = (int)(q % 2);
-    q /= 2;
     const int ks = (int)(q % KS);
     q /= KS;
-    const int g = (int)(q % NG);
-    const int e = (int)(q / NG);
+    const int c = (int)(q % NF);
+    const int e = (int)(q / NF);
     const int k0 = 16 * ks + 8 * (lane >> 5);
-    const int c = lane & 31;
+    const int col = lane & 31;
     u32x4 v;
     if constexpr (WHICH == 0) {
-        const int fc = 32 * g + c;  // intermediate index
+        const int f = col >> 4;                // 0 = gate, 1 = up
+        const int fc = 16 * c + (col & 15);    // intermediate index
         if constexpr (LAYOUT == kLayoutConcat) {  // [E, 2F, H]: gate row fc, up row F + fc
             v = *reinterpret_cast<const u32x4*>(src + ((long long)e * 2 * F + f * F + fc) * H + k0);
         } else {  // [E, H, 2F]: gate column 2fc, up column 2fc + 1
@@ -82,7 +87,7 @@ __global__ __launch_bounds__(256) void moe_pack_kernel(const uint16_t* __restric
                       t[6] | (uint32_t)t[7] << 16};
         }
     } else {
-        const int n = 64 * g + 32 * f + c;  // output (hidden) index
+        const int n = 32 * c + col;  // output (hidden) index
         if constexpr (LAYOUT == kLayoutConcat) {  // [E, H, F]
             v = *reinterpret_cast<const u32x4*>(src + ((long long)e * H + n) * F + k0);
         } else {  // [E, F, H]
@@ -93,7 +98,7 @@ __global__ __launch_bounds__(256) void moe_pack_kernel(const uint16_t* __restric
                       t[6] | (uint32_t)t[7] << 16};
         }
     }
-    *reinterpret_cast<u32x4*>(dst + packed_frag(e, g, ks, f, NG, KS) * kPkFrag + lane * 8) = v;
+    *reinterpret_cast<u32x4*>(dst + packed_frag(e, c, ks, NF, KS) * kPkFrag + lane * 8) = v;
 }
 
 size_t packed_weight_bytes(int H, int F, int E, int which) {
@@ -102,7 +107,7 @@ size_t packed_weight_bytes(int H, int F, int E, int which) {
 }
 
 hipError_t launch_pack(const uint16_t* src, uint16_t* dst, int E, int H, int F, int layout, int which, hipStream_t s) {
-    const long long chunks = (long long)E * (which == 0 ? 2LL * F * H : (long long)H * F) / 8;
+    const long long chunks = (long long)E * (which == 0 ? 2LL * F * H : (long long)H * F) / 8;  // = E*NF*KS*64
     const unsigned grid = (unsigned)((chunks + 255) / 256);
     if (which == 0) {
         if (layout == kLayoutConcat) hipLaunchKernelGGL((moe_pack_kernel<0, kLayoutConcat>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F);
@@ -127,14 +132,13 @@ struct PkParams {
     const int32_t* meta;           // [0] = M-tiles
     const float* route_w;          // [P] (GEMM2)
     void* out;                     // GEMM1: glu bf16 [P, F]; GEMM2: Y fp32 [P, H]
-    int Kd, NG, KS, n_tiles;
+    int Kd, NF, KS, n_tiles;
     int F, H, topk;
     int bias_interleaved;          // GEMM1 bias order: 0 = [gate F | up F], 1 = gate/up interleaved
 };
 
 template <int N>
 using IC = std::integral_constant<int, N>;
-
 
 template <int MODE, int ACT, bool HAS_BIAS>
 __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams prm) {
@@ -161,9 +165,9 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         if (off >= per || it >= it_end) break;
         const WorkItem wi = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
         const int e = wi.e, row_begin = wi.row_begin, rows = wi.rows;
-        const int g = wi.n_idx * kPkWaves + wave;
+        const int fc = wi.n_idx * kPkWaves + wave;
         const int nmb = ceil_div(rows, 32);  // non-empty 32-row blocks
-        const bool active = g < prm.NG;      // wave-uniform: this wave stores results
+        const bool active = fc < prm.NF;     // wave-uniform: this wave stores results
 
         __syncthreads();  // the previous item is done with the LDS buffers and the pair table
         if constexpr (MODE == kModePkDown) {
@@ -173,141 +177,166 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 s_w[tid] = prm.route_w[p];
             }
         }
-        // A rows: thread t loads 16-byte chunk t%8 of rows t/8 and t/8 + 64 of each stage; a wave
-        // instruction covers 8 rows x 128 B.
+        // A rows: thread t loads 16-byte chunk t%8 of rows t/8 + 64i of each stage; a wave instruction
+        // covers 8 rows x 128 B. Rows past the item's end re-read its last row.
         const int a_chunk = tid & 7;
-        const uint16_t* a_src[2];
+        const uint16_t* a_src[kPkMB / 2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kPkMB / 2; ++i) {
             const int ra = min((tid >> 3) + 64 * i, rows - 1);
             long long src_row;
             if constexpr (MODE == kModePkGateUp) src_row = prm.sorted_pairs[row_begin + ra] / prm.topk;
             else src_row = row_begin + ra;
             a_src[i] = prm.A + src_row * Kd + a_chunk * 8;
         }
-        const int gc = g < prm.NG ? g : wi.n_idx * kPkWaves;  // idle waves read the tile's first group
-        const int nw = min(4, prm.NG - 4 * (gc >> 2));
-        const uint16_t* b_ptr = prm.B + packed_frag(e, gc, 0, 0, prm.NG, prm.KS) * kPkFrag + lane * 8;
-        const long long b_step = (long long)nw * 2 * kPkFrag;  // elements between consecutive k-steps
+        const int fcc = active ? fc : wi.n_idx * kPkWaves;  // idle waves read the tile's first fragment
+        const int nw = min(kPkWaves, prm.NF - kPkWaves * wi.n_idx);
+        const uint16_t* b_ptr = prm.B + packed_frag(e, fcc, 0, prm.NF, prm.KS) * kPkFrag + lane * 8;
+        const long long b_step = (long long)nw * kPkFrag;  // elements between consecutive k-steps
 
-        f32x16 acc[kPkMB][2];
+        f32x16 acc[kPkMB];
 #pragma unroll
         for (int mb = 0; mb < kPkMB; ++mb)
 #pragma unroll
-            for (int f = 0; f < 2; ++f)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[mb][f][r] = 0.f;
+            for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
 
-        // Activation chunks in a two-slot register ring (loaded two stages before their MFMAs,
-        // written to LDS one stage before); weight fragments in one slot per k-step, refilled with the
-        // next stage's k-step as soon as its MFMAs have read it (one stage ahead). Every load is visible to the compiler, which waits for exactly the loads each
-        // use needs. Loads are never behind a branch, so those waits stay exact: past the last stage
-        // a step re-reads the last stage (an L2 hit), and a wave whose column group is past the end
-        // loads valid fragments of the tile, skips its MFMAs and stores nothing.
-        u32x4 aring[2][2];
-        u32x4 breg[4][2];  // k-step q of the current stage, refilled with k-step q of the next
-        auto load_a = [&](int s, auto rc) {
-            constexpr int r = decltype(rc)::value;
-            const int sc = min(s, nst - 1);
+        // Activation chunks are loaded at the start of the step before their MFMAs and written to
+        // LDS at its end. Weight fragments sit in kPkBDepth register slots of four k-steps; k-step q
+        // of slot d is refilled with the stage kPkBDepth ahead as soon as its MFMAs have read it.
+        // Every load is visible to the compiler, which waits for exactly the loads each use needs.
+        // Loads and MFMAs are never behind a branch, so those waits stay exact and the loop is one
+        // basic block: past the last stage a step re-reads the last stage (an L2 hit), and a wave
+        // whose fragment is past the end (only in a projection's last N-tile) computes on valid
+        // fragments of the tile and stores nothing.
+        auto kloop = [&](auto nc) {
+            constexpr int NMB = decltype(nc)::value;  // 32-row blocks computed
+            constexpr int NA = (NMB + 1) / 2;         // activation chunks per thread per stage
+            u32x4 areg[NA];
+            u32x4 breg[kPkBDepth][4];
+            auto load_a = [&](int s) {
+                const int sc = min(s, nst - 1);
 #pragma unroll
-            for (int i = 0; i < 2; ++i) aring[r][i] = *reinterpret_cast<const u32x4*>(a_src[i] + sc * kBK);
-        };
-        auto load_b = [&](int s, int q) {  // k-step q of stage s
-            const uint16_t* bp = b_ptr + (long long)(4 * min(s, nst - 1) + q) * b_step;
+                for (int i = 0; i < NA; ++i) areg[i] = *reinterpret_cast<const u32x4*>(a_src[i] + sc * kBK);
+            };
+            auto load_b = [&](int s, auto dc, int q) {  // k-step q of stage s into slot d
+                constexpr int d = decltype(dc)::value;
+                const uint16_t* bp = b_ptr + (long long)(4 * min(s, nst - 1) + q) * b_step;
+                breg[d][q] = *reinterpret_cast<const u32x4*>(bp);
+            };
+            auto store_a = [&](auto bc) {  // the loaded activation chunks -> LDS buffer b
+                constexpr int b = decltype(bc)::value;
+                unsigned char* sA = smem + b * kPkABytes;
 #pragma unroll
-            for (int f = 0; f < 2; ++f) breg[q][f] = *reinterpret_cast<const u32x4*>(bp + f * kPkFrag);
-        };
-        auto store_a = [&](auto rc) {  // activation chunks of ring slot r -> LDS buffer r
-            constexpr int r = decltype(rc)::value;
-            unsigned char* sA = smem + r * kPkABytes;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                *reinterpret_cast<u32x4*>(sA + lds_off((tid >> 3) + 64 * i, a_chunk)) = aring[r][i];
-        };
-        auto kloop = [&](auto nmbc) {
-            constexpr int NMB = decltype(nmbc)::value;
-            // One A fragment register per 32-row block: right after the two MFMAs of block mb at
-            // k-step q consume it, it is reloaded with block mb's fragment of k-step q + 1, which then
-            // has the other blocks' MFMAs to arrive. The next stage's weight loads are spread over the
-            // four k-steps (fenced with sched_barrier) so that the CU's address unit works on them
-            // while the matrix cores run, instead of all waves queueing their loads at once.
-            auto step = [&](int s, auto c0, auto c1) {
-                constexpr int b = decltype(c0)::value;
+                for (int i = 0; i < NA; ++i)
+                    *reinterpret_cast<u32x4*>(sA + lds_off((tid >> 3) + 64 * i, a_chunk)) = areg[i];
+            };
+            // One A fragment register per 32-row block: right after block mb's MFMA at k-step q
+            // consumes it, it is reloaded with block mb's fragment of k-step q + 1, which then has
+            // the other blocks' MFMAs to arrive. The weight loads of the stage kPkBDepth ahead are
+            // spread over the four k-steps (fenced with sched_barrier) so that the CU's address
+            // unit works on them while the matrix cores run.
+            auto step = [&](int s, auto bc, auto dc) {
+                constexpr int b = decltype(bc)::value;
+                constexpr int d = decltype(dc)::value;
                 __syncthreads();  // stage s is in LDS buffer b; every wave is done with the other buffer
                 const unsigned char* sA = smem + b * kPkABytes;
                 auto read_af = [&](int q, int mb) {
                     return *reinterpret_cast<const bf16x8*>(sA + lds_off(mb * 32 + (lane & 31), 2 * q + (lane >> 5)));
                 };
-                load_a(s + 2, c0);  // into the slot stage s's chunks left
+                load_a(s + 1);  // mostly L2 hits: arrive within this step's MFMAs
                 bf16x8 af[NMB];
 #pragma unroll
                 for (int mb = 0; mb < NMB; ++mb) af[mb] = read_af(0, mb);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     __builtin_amdgcn_sched_barrier(0);
-                    const bf16x8 b0 = __builtin_bit_cast(bf16x8, breg[q][0]);
-                    const bf16x8 b1 = __builtin_bit_cast(bf16x8, breg[q][1]);
+                    const bf16x8 bq = __builtin_bit_cast(bf16x8, breg[d][q]);
 #pragma unroll
                     for (int mb = 0; mb < NMB; ++mb) {
-                        if (active) {  // wave-uniform, no loads inside: the compiler's waits stay exact
-                            acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], b0, acc[mb][0], 0, 0, 0);
-                            acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], b1, acc[mb][1], 0, 0, 0);
-                        }
+                        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], bq, acc[mb], 0, 0, 0);
                         if (q + 1 < 4) af[mb] = read_af(q + 1, mb);
                     }
-                    load_b(s + 1, q);  // k-step q of the next stage into the registers just consumed
+                    load_b(s + kPkBDepth, dc, q);  // the registers just consumed
+                    // Keep the order written above: MFMA, then the LDS read that refills its A
+                    // register, block by block; then the weight load.
+#pragma unroll
+                    for (int mb = 0; mb < NMB; ++mb) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
+                        if (q + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                store_a(c1);  // stage s+1's chunks -> the other LDS buffer
+                store_a(IC<1 - b>{});  // stage s+1's chunks -> the other LDS buffer
             };
-            load_a(0, IC<0>{});
-            load_a(1, IC<1>{});
+            load_a(0);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) load_b(0, q);
+            for (int q = 0; q < 4; ++q) load_b(0, IC<0>{}, q);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) load_b(1, IC<1>{}, q);
             store_a(IC<0>{});
             int s = 0;
             for (; s + 1 < nst; s += 2) {
-                step(s, IC<0>{}, IC<1>{});
-                step(s + 1, IC<1>{}, IC<0>{});
+                step(s, IC<0>{}, IC<0>{});
+                step(s + 1, IC<1>{}, IC<1>{});
             }
-            if (s < nst) step(s, IC<0>{}, IC<1>{});
+            if (s < nst) step(s, IC<0>{}, IC<0>{});
         };
+        static_assert(kPkBDepth == 2, "the k-loop above alternates two weight slots");
         switch (nmb) {
             case 1: kloop(IC<1>{}); break;
             case 2: kloop(IC<2>{}); break;
             case 3: kloop(IC<3>{}); break;
-            default: kloop(IC<4>{}); break;
+            case 4: kloop(IC<4>{}); break;
+            case 5: kloop(IC<5>{}); break;
+            case 6: kloop(IC<6>{}); break;
+            case 7: kloop(IC<7>{}); break;
+            default: kloop(IC<8>{}); break;
         }
 
         // ---- epilogue. Element r of a 32x32 accumulator block is at row 8*(r/4) + 4*(lane/32) + (r%4),
         // column lane & 31.
         if constexpr (MODE == kModePkGateUp) {
-            // SwiGLU in registers, the bf16 tile staged in LDS, then written as 16-byte chunks: each
-            // output row of the N-tile is one contiguous 512-byte run.
+            // Columns 0-15 of the fragment are gate, 16-31 the matching up columns. v_permlane16_swap
+            // exchanges lanes 16-31 (48-63) of accumulator element r with lanes 0-15 (32-47) of
+            // element r+4 (8 rows further down): afterwards every lane holds gate and up of one
+            // (row, glu column), with rows r in lanes 0-15 and 32-47 and rows r+4 in the others.
+            // The bf16 tile is staged in LDS, then written as 16-byte chunks: each output row of the
+            // N-tile is one contiguous 256-byte run.
             if (active) {
-                const int fcol = 32 * g + (lane & 31);
+                const int fcol = 16 * fc + (lane & 15);
                 float bg = 0.f, bu = 0.f;
                 if constexpr (HAS_BIAS) {
                     const float* be = prm.bias + (long long)e * 2 * prm.F;
                     bg = prm.bias_interleaved ? be[2 * fcol] : be[fcol];
                     bu = prm.bias_interleaved ? be[2 * fcol + 1] : be[prm.F + fcol];
                 }
-                uint16_t* ep = s_epi + wave * 32 + (lane & 31);
+                uint16_t* ep = s_epi + wave * 16 + (lane & 15);
+                const int rlane = 4 * (lane >> 5) + 8 * ((lane >> 4) & 1);
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int row = mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        ep[row * kPkEpiStride] = f32_to_bf16_bits(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu));
-                    }
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int r4 = 0; r4 < 4; ++r4) {
+                            const int r = 8 * h + r4;
+                            // __float_as_uint takes the element by value (a bit_cast of an ext-vector
+                            // element lvalue reads element 0 with this compiler).
+                            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[mb][r]),
+                                                                             __float_as_uint(acc[mb][r + 4]), false, false);
+                            const float gate = __uint_as_float(sw[0]);
+                            const float up = __uint_as_float(sw[1]);
+                            const int row = mb * 32 + 16 * h + r4 + rlane;
+                            ep[row * kPkEpiStride] = f32_to_bf16_bits(swiglu<ACT>(gate + bg, up + bu));
+                        }
                 }
             }
             __syncthreads();
             uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            const int col0 = wi.n_idx * kPkWaves * 32;
-            for (int i = tid; i < rows * (kPkWaves * 4); i += kPkThreads) {
-                const int row = i / (kPkWaves * 4), c = i % (kPkWaves * 4);
+            const int col0 = wi.n_idx * kPkGlu;
+            for (int i = tid; i < rows * (kPkGlu / 8); i += kPkThreads) {
+                const int row = i / (kPkGlu / 8), c = i % (kPkGlu / 8);
                 const int col = col0 + 8 * c;
                 if (col < prm.F)
                     *reinterpret_cast<u32x4*>(glu + (long long)(row_begin + row) * prm.F + col) =
@@ -316,24 +345,16 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         } else {
             if (!active) continue;
             float* Y = reinterpret_cast<float*>(prm.out);
-            float bn[2] = {0.f, 0.f};
-            if constexpr (HAS_BIAS) {
-#pragma unroll
-                for (int f = 0; f < 2; ++f) bn[f] = prm.bias[(long long)e * prm.H + 64 * g + 32 * f + (lane & 31)];
-            }
+            const int n = 32 * fc + (lane & 31);
+            float bn = 0.f;
+            if constexpr (HAS_BIAS) bn = prm.bias[(long long)e * prm.H + n];
 #pragma unroll
             for (int mb = 0; mb < kPkMB; ++mb) {
                 if (mb >= nmb) break;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < rows) {
-                        const int p = s_pair[row];
-                        const float w = s_w[row];
-#pragma unroll
-                        for (int f = 0; f < 2; ++f)
-                            Y[(long long)p * prm.H + 64 * g + 32 * f + (lane & 31)] = (acc[mb][f][r] + bn[f]) * w;
-                    }
+                    if (row < rows) Y[(long long)s_pair[row] * prm.H + n] = (acc[mb][r] + bn) * s_w[row];
                 }
             }
         }
@@ -356,7 +377,7 @@ static int pk_cu_count() {
 
 template <int MODE, int ACT, bool HAS_BIAS>
 static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s) {
-    int grid = min(max_tiles * prm.n_tiles, pk_cu_count());
+    int grid = min(max_tiles * prm.n_tiles, pk_cu_count());  // one workgroup per CU
     grid = ceil_div(max(grid, 1), 8) * 8;
     hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     return hipGetLastError();
@@ -395,9 +416,9 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.route_w = route_w;
     g1.out = glu;
     g1.Kd = H;
-    g1.NG = F / 32;
+    g1.NF = F / 16;
     g1.KS = H / 16;
-    g1.n_tiles = ceil_div(g1.NG, kPkWaves);
+    g1.n_tiles = ceil_div(g1.NF, kPkWaves);
     g1.F = F;
     g1.H = H;
     g1.topk = K;
@@ -416,9 +437,9 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.bias = b2;
     g2.out = Y;
     g2.Kd = F;
-    g2.NG = H / 64;
+    g2.NF = H / 32;
     g2.KS = F / 16;
-    g2.n_tiles = ceil_div(g2.NG, kPkWaves);
+    g2.n_tiles = ceil_div(g2.NF, kPkWaves);
     st = b2 ? launch_pk_t<kModePkDown, kActSilu, true>(g2, max_tiles, s)
             : launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;

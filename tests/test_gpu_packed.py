@@ -20,8 +20,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _np_pack(W: np.ndarray, layout: str, which: int, H: int, F: int) -> np.ndarray:
-    """Packed order built group by group: for tile t (4 groups), k-step ks, group w, fragment f,
-    lane l: 8 elements B[16ks + 8(l//32) + j][column of (g, f, l%32)]."""
+    """Packed order built fragment by fragment: for tile t (8 fragments), k-step ks, fragment c,
+    lane l: 8 elements B[16ks + 8(l//32) + j][column of (c, l%32)]. gate_up fragment c holds gate
+    columns 16c..16c+15 then the matching up columns; down fragment c holds columns 32c..32c+31."""
     E = W.shape[0]
     if which == 0:  # B[k][n]: n = gate f or up f
         Bk = np.transpose(W, (0, 2, 1)) if layout == "concat" else W  # [E, H, 2F] (concat: gate|up; interleaved: g,u,...)
@@ -29,24 +30,23 @@ def _np_pack(W: np.ndarray, layout: str, which: int, H: int, F: int) -> np.ndarr
             gate, up = Bk[:, :, :F], Bk[:, :, F:]
         else:
             gate, up = Bk[:, :, 0::2], Bk[:, :, 1::2]
-        NG, KS = F // 32, H // 16
-        col = lambda e, g, f, c: (gate if f == 0 else up)[e, :, 32 * g + c]  # noqa: E731
+        NF, KS = F // 16, H // 16
+        col = lambda e, c, j: (gate if j < 16 else up)[e, :, 16 * c + j % 16]  # noqa: E731
     else:
         Bk = np.transpose(W, (0, 2, 1)) if layout == "concat" else W  # [E, F, H]
-        NG, KS = H // 64, F // 16
-        col = lambda e, g, f, c: Bk[e, :, 64 * g + 32 * f + c]  # noqa: E731
+        NF, KS = H // 32, F // 16
+        col = lambda e, c, j: Bk[e, :, 32 * c + j]  # noqa: E731
     out = []
     for e in range(E):
-        for t in range((NG + 3) // 4):
-            groups = list(range(4 * t, min(4 * t + 4, NG)))
+        for t in range((NF + 7) // 8):
+            frags = list(range(8 * t, min(8 * t + 8, NF)))
             for ks in range(KS):
-                for g in groups:
-                    for f in range(2):
-                        frag = np.empty((64, 8), dtype=W.dtype)
-                        for lane in range(64):
-                            k0 = 16 * ks + 8 * (lane // 32)
-                            frag[lane] = col(e, g, f, lane % 32)[k0:k0 + 8]
-                        out.append(frag.reshape(-1))
+                for c in frags:
+                    frag = np.empty((64, 8), dtype=W.dtype)
+                    for lane in range(64):
+                        k0 = 16 * ks + 8 * (lane // 32)
+                        frag[lane] = col(e, c, lane % 32)[k0:k0 + 8]
+                    out.append(frag.reshape(-1))
     return np.concatenate(out)
 
 
@@ -55,7 +55,7 @@ def _np_pack(W: np.ndarray, layout: str, which: int, H: int, F: int) -> np.ndarr
 def test_pack_layout(device, layout, which):
     from cernels_amd import ops
 
-    H, F, E = 192, 320, 2  # 5 gate_up groups / 3 down groups: partial last tiles
+    H, F, E = 192, 320, 2  # 20 gate_up / 6 down fragments: partial last tiles
     g = torch.Generator().manual_seed(3)
     if which == 0:
         shape = (E, 2 * F, H) if layout == "concat" else (E, H, 2 * F)
@@ -90,7 +90,7 @@ SMALL = [
     (6, 90, 128, 64, 8, 2, "concat", "gptoss", True, 0, 0.0),
     (7, 1, 128, 64, 16, 8, "concat", "silu", False, 0, 0.0),
     (8, 1200, 256, 128, 64, 6, "concat", "silu", False, 0, 1.2),
-    (9, 700, 576, 320, 3, 2, "concat", "silu", False, 0, 0.0),  # 9 and 5 groups: idle waves in the last tile
+    (9, 700, 576, 320, 3, 2, "concat", "silu", False, 0, 0.0),  # 20 and 18 fragments: idle waves in the last tile
 ]
 
 
