@@ -206,6 +206,8 @@ int cernels_moe_experts_packed_staged(const void* x, const void* gate_up_packed,
                            workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
     if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    // The packed GEMMs address x with 32-bit buffer offsets.
+    if ((long long)T * H * 2 >= (1LL << 31)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     const PrefillWs w = prefill_ws(T, H, F, E, K);
     if (workspace_bytes < w.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
     char* base = static_cast<char*>(workspace);

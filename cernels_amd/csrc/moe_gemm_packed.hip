@@ -22,6 +22,8 @@
 //
 // GEMM1 fragments hold 16 gate and the 16 matching up columns, so one wave holds both inputs of the
 // gated activation for its 16 glu columns; a v_permlane16_swap pairs them up in the epilogue.
+#include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "moe_tile.h"
@@ -35,7 +37,6 @@ constexpr int kPkMB = kPkBM / 32;           // 32-row MFMA blocks per item
 constexpr int kPkABytes = kPkBM * kBK * 2;  // 32 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
 constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
-constexpr int kPkEpiStride = kPkGlu + 8;    // bf16 row stride of the GEMM1 output tile in LDS
 constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
 
 constexpr int kModePkGateUp = 0;
@@ -135,17 +136,30 @@ struct PkParams {
     int Kd, NF, KS, n_tiles;
     int F, H, topk;
     int bias_interleaved;          // GEMM1 bias order: 0 = [gate F | up F], 1 = gate/up interleaved
+    int a_bytes;                   // GEMM1: bytes of x (< 2^31, checked by the caller)
+    int fw;                        // fragments per item (<= kPkWaves); waves past fw idle
 };
+
+// Word 3 of a raw buffer descriptor on gfx9-family GPUs (gfx950 included): 32-bit data format,
+// no swizzle, no index stride.
+constexpr int kBufferWord3 = 0x00020000;
 
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-template <int MODE, int ACT, bool HAS_BIAS>
+// MODE/ACT/HAS_BIAS select the projection; XPF: the reduction has at least two stages, and the
+// next item's first stages are loaded during the current item's last two steps (cross-item
+// prefetch); ODD: the number of stages is odd, so consecutive items alternate the parity of their
+// LDS buffer and weight register slot.
+template <int MODE, int ACT, bool HAS_BIAS, bool XPF, bool ODD>
 __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams prm) {
+    static_assert(XPF || ODD, "a single-stage reduction is odd");
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kPkABytes];
-    __shared__ int s_pair[kPkBM];
-    __shared__ float s_w[kPkBM];
-    __shared__ __attribute__((aligned(16))) uint16_t s_epi[MODE == kModePkGateUp ? kPkBM * kPkEpiStride : 8];
+    // Epilogue tables, double-buffered by item parity: row -> pair and routing weight (GEMM2), and
+    // the N-tile's bias (GEMM1: 128 gate then 128 up entries; GEMM2: 256 columns).
+    __shared__ int s_pair[2][kPkBM];
+    __shared__ float s_w[2][kPkBM];
+    __shared__ __attribute__((aligned(16))) float s_bias[2][2 * kPkGlu];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
@@ -155,208 +169,334 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const int per = ceil_div(total, 8);
     const int it_end = min(total, (xcd + 1) * per);
     const int Kd = prm.Kd, nst = Kd / kBK;
+    const int a_chunk = tid & 7;
 
     // Items of XCD x are [x*per, x*per + per), handed to its slots in snake order (slot s takes
     // s, 2*slots-1-s, 2*slots+s, ...) so that long and short items mix on every CU, while the items
     // that share a weight tile (neighbours in the list) still run at the same time on one XCD.
-    for (int j = 0;; ++j) {
+    auto item_of = [&](int j, WorkItem& w) {
         const int off = (j & 1) ? (j + 1) * slots - 1 - slot : j * slots + slot;
         const int it = xcd * per + off;
-        if (off >= per || it >= it_end) break;
-        const WorkItem wi = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
-        const int e = wi.e, row_begin = wi.row_begin, rows = wi.rows;
-        const int fc = wi.n_idx * kPkWaves + wave;
-        const int nmb = ceil_div(rows, 32);  // non-empty 32-row blocks
-        const bool active = fc < prm.NF;     // wave-uniform: this wave stores results
-
-        __syncthreads();  // the previous item is done with the LDS buffers and the pair table
-        if constexpr (MODE == kModePkDown) {
-            if (tid < rows) {
-                const int p = prm.sorted_pairs[row_begin + tid];
-                s_pair[tid] = p;
-                s_w[tid] = prm.route_w[p];
-            }
+        if (off >= per || it >= it_end) return false;
+        w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
+        return true;
+    };
+    // Operands are read with buffer loads: a 128-bit descriptor per operand and item (uniform,
+    // SGPRs) plus a 32-bit per-lane offset, so the k-loop holds no 64-bit addresses.
+    //   A: GEMM1 gathers token rows of x (descriptor over all of x); GEMM2 reads the item's own
+    //      contiguous glu rows (descriptor at its first row). Thread t reads rows t/8 + 64i of the
+    //      tile, clamped to the item's last row: a_row() is the row in the A matrix, a_off() its byte
+    //      offset from the descriptor base.
+    //   B: the wave's fragment run from k-step 0; lane offset lane*16, k-step offsets uniform.
+    auto a_row = [&](const WorkItem& w, int i) { return w.row_begin + min((tid >> 3) + 64 * i, w.rows - 1); };
+    auto a_off = [&](const WorkItem& w, int src_row) {
+        const int r = MODE == kModePkGateUp ? src_row : src_row - w.row_begin;
+        return (uint32_t)r * (uint32_t)(Kd * 2) + (uint32_t)a_chunk * 16u;
+    };
+    auto a_rsrc = [&](const WorkItem& w) {
+        if constexpr (MODE == kModePkGateUp)
+            return __builtin_amdgcn_make_buffer_rsrc((void*)prm.A, (short)0, prm.a_bytes, kBufferWord3);
+        else
+            return __builtin_amdgcn_make_buffer_rsrc((void*)(prm.A + (long long)w.row_begin * Kd), (short)0,
+                                                     w.rows * Kd * 2, kBufferWord3);
+    };
+    // This wave's fragment of an item; waves past the item's fragments (or past NF) are idle and
+    // never load weights. Fragments are stored in bundles of eight, k-step-major inside a bundle.
+    auto frag_of = [&](const WorkItem& w) { return min(w.n_idx * prm.fw + wave, prm.NF - 1); };
+    auto b_rsrc = [&](const WorkItem& w) {
+        const int fc = frag_of(w);
+        const int nw = min(8, prm.NF - 8 * (fc >> 3));
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(prm.B + packed_frag(w.e, fc, 0, prm.NF, prm.KS) * kPkFrag),
+                                                 (short)0, (prm.KS - 1) * nw * kPkFrag * 2 + 1024, kBufferWord3);
+    };
+    auto b_stride = [&](const WorkItem& w) { return min(8, prm.NF - 8 * (frag_of(w) >> 3)) * kPkFrag * 2; };
+    // Table entries of an item for thread t (row t; bias entry t).
+    auto tab_pair = [&](const WorkItem& w) { return prm.sorted_pairs[w.row_begin + min(tid, w.rows - 1)]; };
+    auto tab_bias = [&](const WorkItem& w) {
+        if constexpr (MODE == kModePkGateUp) {
+            const int f = (tid >> 7) & 1, col = min(w.n_idx * 16 * prm.fw + (tid & (kPkGlu - 1)), prm.F - 1);
+            const float* be = prm.bias + (long long)w.e * 2 * prm.F;
+            return prm.bias_interleaved ? be[2 * col + f] : be[f * prm.F + col];
+        } else {
+            const int col = min(w.n_idx * 32 * prm.fw + (tid & (2 * kPkGlu - 1)), prm.H - 1);
+            return prm.bias[(long long)w.e * prm.H + col];
         }
-        // A rows: thread t loads 16-byte chunk t%8 of rows t/8 + 64i of each stage; a wave instruction
-        // covers 8 rows x 128 B. Rows past the item's end re-read its last row.
-        const int a_chunk = tid & 7;
-        const uint16_t* a_src[kPkMB / 2];
+    };
+    auto tab_store = [&](int buf, int pair, float w, float bias) {
+        if (tid < kPkBM) {
+            if constexpr (MODE == kModePkDown) {
+                s_pair[buf][tid] = pair;
+                s_w[buf][tid] = w;
+            }
+            if constexpr (HAS_BIAS) s_bias[buf][tid] = bias;
+        }
+    };
+
+    WorkItem cur;
+    if (!item_of(0, cur)) return;
+    uint32_t a_cur[kPkMB / 2];  // activation row offsets of the current item
+    __amdgpu_buffer_rsrc_t ra_cur = a_rsrc(cur), rb_cur = b_rsrc(cur);
+    int bstep_cur = b_stride(cur);  // bytes between k-steps
+    const uint32_t b_lane = (uint32_t)lane * 16u;
+
+    f32x16 acc[kPkMB];
+    u32x4 areg[kPkMB / 2];  // activation chunks of the next stage
+    u32x4 breg[2][4];       // weight fragments: slot d holds the four k-steps of one stage
+    auto a_ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t ao, int stage) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, ao, stage * kBK * 2, 0));
+    };
+    auto b_ld = [&](__amdgpu_buffer_rsrc_t r, int bs, int stage, int q) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_lane, (4 * stage + q) * bs, 0));
+    };
+    auto store_a = [&](auto nc, auto bc) {  // the first n loaded activation chunks -> LDS buffer b
+        constexpr int n = decltype(nc)::value, b = decltype(bc)::value;
+        unsigned char* sA = smem + b * kPkABytes;
+#pragma unroll
+        for (int i = 0; i < n; ++i) *reinterpret_cast<u32x4*>(sA + lds_off((tid >> 3) + 64 * i, a_chunk)) = areg[i];
+    };
+    // The whole set-up of one item without prefetch: offsets, tables into buffer tb, stage 0 into
+    // LDS buffer 0, weight stages 0 and 1 into slots 0 and 1.
+    auto start_item = [&](const WorkItem& w, int tb) {
+        int pr[kPkMB / 2];
 #pragma unroll
         for (int i = 0; i < kPkMB / 2; ++i) {
-            const int ra = min((tid >> 3) + 64 * i, rows - 1);
-            long long src_row;
-            if constexpr (MODE == kModePkGateUp) src_row = prm.sorted_pairs[row_begin + ra] / prm.topk;
-            else src_row = row_begin + ra;
-            a_src[i] = prm.A + src_row * Kd + a_chunk * 8;
+            if constexpr (MODE == kModePkGateUp) pr[i] = prm.sorted_pairs[a_row(w, i)];
+            else pr[i] = a_row(w, i);
         }
-        const int fcc = active ? fc : wi.n_idx * kPkWaves;  // idle waves read the tile's first fragment
-        const int nw = min(kPkWaves, prm.NF - kPkWaves * wi.n_idx);
-        const uint16_t* b_ptr = prm.B + packed_frag(e, fcc, 0, prm.NF, prm.KS) * kPkFrag + lane * 8;
-        const long long b_step = (long long)nw * kPkFrag;  // elements between consecutive k-steps
+        int pair = 0;
+        float rw = 0.f, bias = 0.f;
+        if constexpr (MODE == kModePkDown) pair = tab_pair(w);
+        if constexpr (HAS_BIAS) bias = tab_bias(w);
+#pragma unroll
+        for (int i = 0; i < kPkMB / 2; ++i)
+            a_cur[i] = a_off(w, MODE == kModePkGateUp ? pr[i] / prm.topk : pr[i]);
+        if constexpr (MODE == kModePkDown) rw = prm.route_w[pair];
+#pragma unroll
+        for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_cur, a_cur[i], 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) breg[0][q] = b_ld(rb_cur, bstep_cur, 0, q);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) breg[1][q] = b_ld(rb_cur, bstep_cur, min(1, nst - 1), q);
+        tab_store(tb, pair, rw, bias);
+        __syncthreads();  // without prefetch the previous item's only step may still read buffer 0
+        store_a(IC<kPkMB / 2>{}, IC<0>{});
+    };
+    start_item(cur, 0);
 
-        f32x16 acc[kPkMB];
+    int par = 0;  // LDS buffer / weight slot of the current item's stage 0
+    for (int j = 0;; ++j) {
+        WorkItem nx;
+        const bool has_nx = item_of(j + 1, nx);
+        if (!has_nx) nx = cur;  // past the end the "next" loads re-read the current item
+        const __amdgpu_buffer_rsrc_t ra_nx = a_rsrc(nx), rb_nx = b_rsrc(nx);
+        const int bstep_nx = b_stride(nx);
+        const int row_begin = cur.row_begin, rows = cur.rows;
+        const int fc = cur.n_idx * prm.fw + wave;
+        const bool active = wave < prm.fw && fc < prm.NF;  // wave-uniform
+        const int nmb = ceil_div(rows, 32);  // non-empty 32-row blocks
+        const int tb = j & 1;                // table buffer of this item
 #pragma unroll
         for (int mb = 0; mb < kPkMB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
 
-        // Activation chunks are loaded at the start of the step before their MFMAs and written to
-        // LDS at its end. Weight fragments sit in kPkBDepth register slots of four k-steps; k-step q
-        // of slot d is refilled with the stage kPkBDepth ahead as soon as its MFMAs have read it.
-        // Every load is visible to the compiler, which waits for exactly the loads each use needs.
-        // Loads and MFMAs are never behind a branch, so those waits stay exact and the loop is one
-        // basic block: past the last stage a step re-reads the last stage (an L2 hit), and a wave
-        // whose fragment is past the end (only in a projection's last N-tile) computes on valid
-        // fragments of the tile and stores nothing.
-        auto kloop = [&](auto nc) {
-            constexpr int NMB = decltype(nc)::value;  // 32-row blocks computed
-            constexpr int NA = (NMB + 1) / 2;         // activation chunks per thread per stage
-            u32x4 areg[NA];
-            u32x4 breg[kPkBDepth][4];
-            auto load_a = [&](int s) {
-                const int sc = min(s, nst - 1);
-#pragma unroll
-                for (int i = 0; i < NA; ++i) areg[i] = *reinterpret_cast<const u32x4*>(a_src[i] + sc * kBK);
-            };
-            auto load_b = [&](int s, auto dc, int q) {  // k-step q of stage s into slot d
-                constexpr int d = decltype(dc)::value;
-                const uint16_t* bp = b_ptr + (long long)(4 * min(s, nst - 1) + q) * b_step;
-                breg[d][q] = *reinterpret_cast<const u32x4*>(bp);
-            };
-            auto store_a = [&](auto bc) {  // the loaded activation chunks -> LDS buffer b
+        // The k-loop. Step s runs the MFMAs of stage s from LDS buffer and weight slot (par + s) & 1,
+        // loads the activation chunks of stage s+1 at its start (written to the other buffer at its
+        // end) and, k-step by k-step, the weights of stage s+2 into the slot just consumed. In the
+        // last two steps "stage s+1 / s+2" are stages 0 and 1 of the next item (XPF), whose row
+        // offsets and tables are loaded there too, so the weights keep streaming through the
+        // epilogue. Loads and MFMAs are never behind a branch: the compiler's waits stay exact and
+        // each step is one basic block.
+        auto kloop = [&](auto nc, auto pc) {
+            constexpr int NMB = decltype(nc)::value;  // 32-row blocks computed; 0: idle wave
+            constexpr int PP = decltype(pc)::value;   // parity of stage 0
+            // Activation chunks per thread per stage. The tile is shared: an idle wave still loads
+            // its rows (all four chunks; rows past the item's blocks are never read).
+            constexpr int NA = NMB > 0 ? (NMB + 1) / 2 : kPkMB / 2;
+            int nxr[kPkMB / 2];                       // next item's rows (GEMM1: pair ids), KIND 1 -> 2
+            int npair = 0;
+            float nbias = 0.f;
+            // KIND 0: ordinary step; 1: second to last (next item's weight stage 0, rows, tables);
+            // 2: last (next item's activation stage 0, all 256 rows, and weight stage 1).
+            auto step = [&](int s, auto bc, auto kc) {
                 constexpr int b = decltype(bc)::value;
-                unsigned char* sA = smem + b * kPkABytes;
-#pragma unroll
-                for (int i = 0; i < NA; ++i)
-                    *reinterpret_cast<u32x4*>(sA + lds_off((tid >> 3) + 64 * i, a_chunk)) = areg[i];
-            };
-            // One A fragment register per 32-row block: right after block mb's MFMA at k-step q
-            // consumes it, it is reloaded with block mb's fragment of k-step q + 1, which then has
-            // the other blocks' MFMAs to arrive. The weight loads of the stage kPkBDepth ahead are
-            // spread over the four k-steps (fenced with sched_barrier) so that the CU's address
-            // unit works on them while the matrix cores run.
-            auto step = [&](int s, auto bc, auto dc) {
-                constexpr int b = decltype(bc)::value;
-                constexpr int d = decltype(dc)::value;
+                constexpr int KIND = decltype(kc)::value;
                 __syncthreads();  // stage s is in LDS buffer b; every wave is done with the other buffer
                 const unsigned char* sA = smem + b * kPkABytes;
                 auto read_af = [&](int q, int mb) {
                     return *reinterpret_cast<const bf16x8*>(sA + lds_off(mb * 32 + (lane & 31), 2 * q + (lane >> 5)));
                 };
-                load_a(s + 1);  // mostly L2 hits: arrive within this step's MFMAs
-                bf16x8 af[NMB];
+                float nw = 0.f;
+                if constexpr (KIND == 2) {
+                    if constexpr (XPF) {
 #pragma unroll
-                for (int mb = 0; mb < NMB; ++mb) af[mb] = read_af(0, mb);
+                        for (int i = 0; i < kPkMB / 2; ++i)
+                            a_cur[i] = a_off(nx, MODE == kModePkGateUp ? nxr[i] / prm.topk : nxr[i]);
+#pragma unroll
+                        for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_nx, a_cur[i], 0);
+                        if constexpr (MODE == kModePkDown) nw = prm.route_w[npair];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < NA; ++i) areg[i] = a_ld(ra_cur, a_cur[i], s + 1);
+                    if constexpr (KIND == 1) {
+#pragma unroll
+                        for (int i = 0; i < kPkMB / 2; ++i) {
+                            if constexpr (MODE == kModePkGateUp) nxr[i] = prm.sorted_pairs[a_row(nx, i)];
+                            else nxr[i] = a_row(nx, i);
+                        }
+                        if constexpr (MODE == kModePkDown) npair = tab_pair(nx);
+                        if constexpr (HAS_BIAS) nbias = tab_bias(nx);
+                    }
+                }
+                // A fragments in a ring of R registers: MFMA k (k-step k / NMB, block k % NMB) reads
+                // slot k % R, which is then refilled with fragment k + R, R MFMAs ahead of its use.
+                constexpr int R = NMB < 4 ? (NMB > 0 ? NMB : 1) : 4;
+                constexpr int NK = 4 * NMB;
+                bf16x8 af[R];
+                if constexpr (NMB > 0) {
+#pragma unroll
+                for (int k = 0; k < R; ++k) af[k] = read_af(k / NMB, k % NMB);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     __builtin_amdgcn_sched_barrier(0);
-                    const bf16x8 bq = __builtin_bit_cast(bf16x8, breg[d][q]);
+                    const bf16x8 bq = __builtin_bit_cast(bf16x8, breg[b][q]);
 #pragma unroll
                     for (int mb = 0; mb < NMB; ++mb) {
-                        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], bq, acc[mb], 0, 0, 0);
-                        if (q + 1 < 4) af[mb] = read_af(q + 1, mb);
+                        const int k = q * NMB + mb;
+                        // Weights as the first operand: the accumulator comes out transposed, each lane
+                        // holding four consecutive output columns of one row.
+                        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq, af[k % R], acc[mb], 0, 0, 0);
+                        if (k + R < NK) af[k % R] = read_af((k + R) / NMB, (k + R) % NMB);
                     }
-                    load_b(s + kPkBDepth, dc, q);  // the registers just consumed
+                    if constexpr (KIND == 0) breg[b][q] = b_ld(rb_cur, bstep_cur, s + 2, q);
+                    else if constexpr (XPF) breg[b][q] = b_ld(rb_nx, bstep_nx, KIND - 1, q);
                     // Keep the order written above: MFMA, then the LDS read that refills its A
                     // register, block by block; then the weight load.
 #pragma unroll
                     for (int mb = 0; mb < NMB; ++mb) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
-                        if (q + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // MFMA
+                        if (q * NMB + mb + R < NK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
                     }
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+                    if (KIND == 0 || XPF) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+                }
+                } else if constexpr (KIND != 0 && XPF) {
+                    // An idle wave may be active in the next item: its first two weight stages are
+                    // prefetched all the same.
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) breg[b][q] = b_ld(rb_nx, bstep_nx, KIND - 1, q);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                store_a(IC<1 - b>{});  // stage s+1's chunks -> the other LDS buffer
+                if constexpr (KIND == 2) {
+                    if constexpr (XPF) {
+                        store_a(IC<kPkMB / 2>{}, IC<1 - b>{});
+                        tab_store(tb ^ 1, npair, nw, nbias);
+                    }
+                } else {
+                    store_a(IC<NA>{}, IC<1 - b>{});
+                }
             };
-            load_a(0);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) load_b(0, IC<0>{}, q);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) load_b(1, IC<1>{}, q);
-            store_a(IC<0>{});
+            const int M = nst - 2;  // ordinary steps
             int s = 0;
-            for (; s + 1 < nst; s += 2) {
-                step(s, IC<0>{}, IC<0>{});
-                step(s + 1, IC<1>{}, IC<1>{});
+            for (; s + 1 < M; s += 2) {
+                step(s, IC<PP>{}, IC<0>{});
+                step(s + 1, IC<1 - PP>{}, IC<0>{});
             }
-            if (s < nst) step(s, IC<0>{}, IC<0>{});
+            if constexpr (ODD) {
+                if constexpr (XPF) {
+                    step(s, IC<PP>{}, IC<0>{});  // M is odd
+                    step(nst - 2, IC<1 - PP>{}, IC<1>{});
+                }
+                step(nst - 1, IC<PP>{}, IC<2>{});
+            } else {
+                step(nst - 2, IC<PP>{}, IC<1>{});
+                step(nst - 1, IC<1 - PP>{}, IC<2>{});
+            }
         };
-        static_assert(kPkBDepth == 2, "the k-loop above alternates two weight slots");
-        switch (nmb) {
-            case 1: kloop(IC<1>{}); break;
-            case 2: kloop(IC<2>{}); break;
-            case 3: kloop(IC<3>{}); break;
-            case 4: kloop(IC<4>{}); break;
-            case 5: kloop(IC<5>{}); break;
-            case 6: kloop(IC<6>{}); break;
-            case 7: kloop(IC<7>{}); break;
-            default: kloop(IC<8>{}); break;
+        auto dispatch = [&](auto pc) {
+            if (!active) {
+                kloop(IC<0>{}, pc);
+                return;
+            }
+            switch (nmb) {
+                case 1: kloop(IC<1>{}, pc); break;
+                case 2: kloop(IC<2>{}, pc); break;
+                case 3: kloop(IC<3>{}, pc); break;
+                case 4: kloop(IC<4>{}, pc); break;
+                case 5: kloop(IC<5>{}, pc); break;
+                case 6: kloop(IC<6>{}, pc); break;
+                case 7: kloop(IC<7>{}, pc); break;
+                default: kloop(IC<8>{}, pc); break;
+            }
+        };
+        if constexpr (XPF && ODD) {
+            if (par) dispatch(IC<1>{});
+            else dispatch(IC<0>{});
+        } else {
+            dispatch(IC<0>{});
         }
 
-        // ---- epilogue. Element r of a 32x32 accumulator block is at row 8*(r/4) + 4*(lane/32) + (r%4),
-        // column lane & 31.
-        if constexpr (MODE == kModePkGateUp) {
-            // Columns 0-15 of the fragment are gate, 16-31 the matching up columns. v_permlane16_swap
-            // exchanges lanes 16-31 (48-63) of accumulator element r with lanes 0-15 (32-47) of
-            // element r+4 (8 rows further down): afterwards every lane holds gate and up of one
-            // (row, glu column), with rows r in lanes 0-15 and 32-47 and rows r+4 in the others.
-            // The bf16 tile is staged in LDS, then written as 16-byte chunks: each output row of the
-            // N-tile is one contiguous 256-byte run.
-            if (active) {
-                const int fcol = 16 * fc + (lane & 15);
-                float bg = 0.f, bu = 0.f;
-                if constexpr (HAS_BIAS) {
-                    const float* be = prm.bias + (long long)e * 2 * prm.F;
-                    bg = prm.bias_interleaved ? be[2 * fcol] : be[fcol];
-                    bu = prm.bias_interleaved ? be[2 * fcol + 1] : be[prm.F + fcol];
-                }
-                uint16_t* ep = s_epi + wave * 16 + (lane & 15);
-                const int rlane = 4 * (lane >> 5) + 8 * ((lane >> 4) & 1);
+        // ---- epilogue: element r of a transposed 32x32 accumulator block is row lane & 31 of the
+        // block, column 8*(r/4) + 4*(lane/32) + (r%4) of the fragment. Only LDS reads and global
+        // stores here: a global load would have to wait for the next item's weights in flight.
+        if (active) {
+            const int c4 = 4 * (lane >> 5);
+            if constexpr (MODE == kModePkGateUp) {
+                // Fragment columns 0-15 are gate, 16-31 the matching up columns: elements r (< 8) and
+                // r + 8 of one lane are gate and up of the same glu column.
+                uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
+                    const int row = mb * 32 + (lane & 31);
+                    if (row < rows) {
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
+                        for (int i = 0; i < 2; ++i) {
+                            f32x4 g4 = {0.f, 0.f, 0.f, 0.f}, u4 = {0.f, 0.f, 0.f, 0.f};
+                            if constexpr (HAS_BIAS) {
+                                g4 = *reinterpret_cast<const f32x4*>(&s_bias[tb][16 * wave + 8 * i + c4]);
+                                u4 = *reinterpret_cast<const f32x4*>(&s_bias[tb][kPkGlu + 16 * wave + 8 * i + c4]);
+                            }
+                            float v[4];
 #pragma unroll
-                        for (int r4 = 0; r4 < 4; ++r4) {
-                            const int r = 8 * h + r4;
-                            // __float_as_uint takes the element by value (a bit_cast of an ext-vector
-                            // element lvalue reads element 0 with this compiler).
-                            const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[mb][r]),
-                                                                             __float_as_uint(acc[mb][r + 4]), false, false);
-                            const float gate = __uint_as_float(sw[0]);
-                            const float up = __uint_as_float(sw[1]);
-                            const int row = mb * 32 + 16 * h + r4 + rlane;
-                            ep[row * kPkEpiStride] = f32_to_bf16_bits(swiglu<ACT>(gate + bg, up + bu));
+                            for (int jj = 0; jj < 4; ++jj)
+                                v[jj] = swiglu<ACT>(acc[mb][4 * i + jj] + g4[jj], acc[mb][8 + 4 * i + jj] + u4[jj]);
+                            *reinterpret_cast<u32x2*>(glu + (long long)(row_begin + row) * prm.F + 16 * fc + 8 * i + c4) =
+                                u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                         }
+                    }
+                }
+            } else {
+                float* Y = reinterpret_cast<float*>(prm.out);
+#pragma unroll
+                for (int mb = 0; mb < kPkMB; ++mb) {
+                    if (mb >= nmb) break;
+                    const int row = mb * 32 + (lane & 31);
+                    if (row < rows) {
+                        const int p = s_pair[tb][row];
+                        const float w = s_w[tb][row];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            f32x4 bn = {0.f, 0.f, 0.f, 0.f};
+                            if constexpr (HAS_BIAS) bn = *reinterpret_cast<const f32x4*>(&s_bias[tb][32 * wave + 8 * i + c4]);
+                            f32x4 v;
+#pragma unroll
+                            for (int jj = 0; jj < 4; ++jj) v[jj] = (acc[mb][4 * i + jj] + bn[jj]) * w;
+                            *reinterpret_cast<f32x4*>(Y + (long long)p * prm.H + 32 * fc + 8 * i + c4) = v;
+                        }
+                    }
                 }
             }
-            __syncthreads();
-            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            const int col0 = wi.n_idx * kPkGlu;
-            for (int i = tid; i < rows * (kPkGlu / 8); i += kPkThreads) {
-                const int row = i / (kPkGlu / 8), c = i % (kPkGlu / 8);
-                const int col = col0 + 8 * c;
-                if (col < prm.F)
-                    *reinterpret_cast<u32x4*>(glu + (long long)(row_begin + row) * prm.F + col) =
-                        *reinterpret_cast<const u32x4*>(s_epi + row * kPkEpiStride + 8 * c);
-            }
+        }
+        if (!has_nx) break;
+        cur = nx;
+        ra_cur = ra_nx;
+        rb_cur = rb_nx;
+        bstep_cur = bstep_nx;
+        if constexpr (XPF) {
+            if constexpr (ODD) par ^= 1;
         } else {
-            if (!active) continue;
-            float* Y = reinterpret_cast<float*>(prm.out);
-            const int n = 32 * fc + (lane & 31);
-            float bn = 0.f;
-            if constexpr (HAS_BIAS) bn = prm.bias[(long long)e * prm.H + n];
-#pragma unroll
-            for (int mb = 0; mb < kPkMB; ++mb) {
-                if (mb >= nmb) break;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < rows) Y[(long long)s_pair[row] * prm.H + n] = (acc[mb][r] + bn) * s_w[row];
-                }
-            }
+            start_item(cur, tb ^ 1);
         }
     }
 }
@@ -379,7 +519,13 @@ template <int MODE, int ACT, bool HAS_BIAS>
 static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s) {
     int grid = min(max_tiles * prm.n_tiles, pk_cu_count());  // one workgroup per CU
     grid = ceil_div(max(grid, 1), 8) * 8;
-    hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    const int nst = prm.Kd / kBK;
+    if (nst >= 2 && (nst & 1) == 0)
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    else if (nst >= 2)
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, true>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    else
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, false, true>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     return hipGetLastError();
 }
 
@@ -390,6 +536,32 @@ hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int
                           hipStream_t s);
 
 int packed_tile_m() { return kPkBM; }
+
+// Fragments per item. Items of one projection all have the same cost, so a launch takes
+// ceil(items / CUs) rounds; narrower items (fewer active waves) cut the last, partly empty round at
+// the price of more items. Estimated from the shape alone (rows per expert P/E, no device sync): an
+// item stage costs max(weight streaming ~ fw, MFMA of the busiest SIMD ~ ceil(fw/4) * blocks), plus
+// a fixed epilogue per item. Prefers wider items unless a narrower one is 2% cheaper.
+static int pick_fw(long long P, int E, int NF, int Kd, int cus) {
+    const double r = (double)P / E;
+    const int mt_e = std::max(1, (int)std::ceil(r / kPkBM));                       // M-tiles per expert
+    const int nmb = std::max(1, (int)std::ceil(std::min<double>(kPkBM, r) / 32));  // blocks per M-tile
+    const long long mtiles = (long long)E * mt_e;
+    const int nst = Kd / kBK;
+    double best = 0;
+    int best_w = kPkWaves;
+    for (int w = kPkWaves; w >= 1; --w) {
+        const long long items = mtiles * ceil_div(NF, w);
+        const long long rounds = (items + cus - 1) / cus;
+        const double stage = std::max(w * 175.0 / mt_e, ceil_div(w, 4) * nmb * 64.0);
+        const double cost = rounds * (nst * stage + 2000.0);
+        if (w == kPkWaves || cost < best * 0.98) {
+            best = cost;
+            best_w = w;
+        }
+    }
+    return best_w;
+}
 
 // route -> packed gate_up GEMM -> packed down GEMM -> combine, all on stream s. Shapes were checked
 // by the caller (H % 64 == 0, F % 64 == 0, E <= 1024, T >= 1).
@@ -418,11 +590,13 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.Kd = H;
     g1.NF = F / 16;
     g1.KS = H / 16;
-    g1.n_tiles = ceil_div(g1.NF, kPkWaves);
+    g1.fw = pick_fw((long long)T * K, E, g1.NF, H, pk_cu_count());
+    g1.n_tiles = ceil_div(g1.NF, g1.fw);
     g1.F = F;
     g1.H = H;
     g1.topk = K;
     g1.bias_interleaved = bias_interleaved;
+    g1.a_bytes = T * H * 2;
     if (act == kActSilu)
         st = b1 ? launch_pk_t<kModePkGateUp, kActSilu, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActSilu, false>(g1, max_tiles, s);
@@ -439,7 +613,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.Kd = F;
     g2.NF = H / 32;
     g2.KS = F / 16;
-    g2.n_tiles = ceil_div(g2.NF, kPkWaves);
+    g2.fw = pick_fw((long long)T * K, E, g2.NF, F, pk_cu_count());
+    g2.n_tiles = ceil_div(g2.NF, g2.fw);
     st = b2 ? launch_pk_t<kModePkDown, kActSilu, true>(g2, max_tiles, s)
             : launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;
