@@ -7,12 +7,13 @@
 // is atomic-ordered and so varies run to run; this one is the op_eager order (expert, then top-k
 // slot, then token), identical on every call.
 //
-// Three launches, a classic radix-sort pass over the routed pairs visited in slot-major order
-// q = k*T + t and cut into tiles of 1024:
+// A classic radix-sort pass over the routed pairs visited in slot-major order q = k*T + t and cut
+// into tiles of 1024:
 //   count   (one workgroup per tile)  per-tile expert histogram -> counts[tile][E]
 //   scan    (one workgroup)           per expert, exclusive scan over tiles (in place: the
 //                                     absolute first write position of each tile), then over
 //                                     experts -> offsets, tile list
+//   (count and scan run as one single-workgroup launch while the per-tile histograms fit in LDS)
 //   scatter (one workgroup per tile)  per-wave histograms inside the tile give each wave its
 //                                     write cursors; each wave scatters its 256 pairs in order,
 //                                     ranking lanes that share an expert with a bit-sliced ballot
@@ -171,6 +172,64 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_scatter_kernel(const int
     }
 }
 
+// Count and scan fused in one workgroup: per-tile expert histograms are built in LDS with LDS
+// atomics (thread t takes pairs t, t+1024, ... so iteration i is tile i), then scanned per expert
+// over tiles and over experts exactly as in moe_route_scan_kernel. Used while the histograms fit in
+// LDS (ntiles * E <= kRtFusedCells), which saves a launch and a pass over global memory.
+constexpr int kRtFusedCells = 28 * 1024;
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
+    const int32_t* __restrict__ idx, int T, int K, int E, int BM, int ntiles, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
+    int32_t* __restrict__ meta) {
+    __shared__ int32_t h[kRtFusedCells];  // [ntiles][E]
+    __shared__ int32_t s_off[kRouteThreads];
+    __shared__ int wave_tot[kRouteWaves];
+    const int tid = threadIdx.x, P = T * K;
+    for (int i = tid; i < ntiles * E; i += kRouteThreads) h[i] = 0;
+    __syncthreads();
+    // Eight pairs per thread are loaded before any of their LDS atomics, so the loads overlap.
+    for (int q0 = tid; q0 < P; q0 += 8 * kRouteThreads) {
+        int ev[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u * kRouteThreads;
+            ev[u] = q < P ? expert_at(idx, q, T, K, E) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (ev[u] >= 0) atomicAdd(&h[((q0 + u * kRouteThreads) / kRtTile) * E + ev[u]], 1);
+    }
+    __syncthreads();
+    const int e = tid;  // E <= kRouteThreads is checked on the host
+    int run = 0;
+    if (e < E) {
+        for (int t = 0; t < ntiles; ++t) {
+            const int c = h[t * E + e];
+            h[t * E + e] = run;
+            run += c;
+        }
+    }
+    int valid_total = 0, tiles_total = 0;
+    const int off = block_exclusive_scan(run, wave_tot, &valid_total);
+    const int nt = ceil_div(run, BM);
+    const int toff = block_exclusive_scan(nt, wave_tot, &tiles_total);
+    if (e < E) {
+        offsets[e] = off;
+        tile_offsets[e] = toff;
+        s_off[e] = off;
+        for (int j = 0; j < nt; ++j) tile_expert[toff + j] = e;
+    }
+    __syncthreads();  // every expert's prefix over tiles is in h, its offset in s_off
+    for (int i = tid; i < ntiles * E; i += kRouteThreads) counts[i] = h[i] + s_off[i % E];  // absolute positions
+    if (tid == 0) {
+        offsets[E] = valid_total;
+        tile_offsets[E] = tiles_total;
+        meta[0] = tiles_total;
+        meta[1] = valid_total;
+    }
+}
+
 int route_tiles(int T, int K) { return ceil_div(T * K, kRtTile); }
 size_t route_workspace_bytes(int T, int K, int E) { return (size_t)max(route_tiles(T, K), 1) * E * sizeof(int32_t); }
 
@@ -178,11 +237,15 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
                         hipStream_t stream) {
     const int nt = route_tiles(T, K);
-    if (nt > 0)
+    if ((long long)nt * E <= kRtFusedCells) {
+        hipLaunchKernelGGL(moe_route_count_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, idx, T, K, E, BM, nt,
+                           counts, offsets, tile_offsets, tile_expert, meta);
+    } else {
         hipLaunchKernelGGL(moe_route_count_kernel, dim3(nt), dim3(kRtThreads), E * sizeof(int32_t), stream, idx, T, K,
                            E, counts);
-    hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, counts, nt, E, BM, offsets,
-                       tile_offsets, tile_expert, meta);
+        hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, counts, nt, E, BM, offsets,
+                           tile_offsets, tile_expert, meta);
+    }
     if (nt > 0)
         hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nt), dim3(kRtThreads), 4 * E * sizeof(int32_t), stream, idx,
                            T, K, E, counts, sorted_pairs);
