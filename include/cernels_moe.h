@@ -107,7 +107,8 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
  *          (src [E,H,F] concat or [E,F,H] interleaved).
  *   bias_layout (experts_packed): column order of gate_up_bias, CERNELS_MOE_LAYOUT_CONCAT
  *          ([gate F | up F]) or CERNELS_MOE_LAYOUT_INTERLEAVED (gate/up alternating).
- * Limits: H % 64 == 0, F % 64 == 0, E <= 1024. */
+ * Limits: H % 64 == 0, F % 64 == 0, E <= 1024; experts_packed also T*H*2 < 2^31 (32-bit offsets).
+ * Otherwise CERNELS_MOE_UNSUPPORTED_SHAPE. */
 size_t cernels_moe_packed_weight_bytes(int32_t H, int32_t F, int32_t E, int32_t which);
 int cernels_moe_pack_weights(const void* src, int32_t H, int32_t F, int32_t E, int32_t layout, int32_t which,
                              void* dst, hipStream_t stream);
