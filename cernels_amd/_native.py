@@ -27,6 +27,7 @@ STATUS = {
 LAYOUT_CONCAT, LAYOUT_INTERLEAVED = 0, 1
 ACT_SILU, ACT_GPTOSS = 0, 1
 GATE_UP, DOWN = 0, 1
+ROUTER_SOFTMAX_TOPK, ROUTER_TOPK_SOFTMAX = 0, 1
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int32
@@ -59,6 +60,7 @@ _SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P, _P],
     ),
+    "cernels_moe_router": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "cernels_moe_decode_max_tokens": (_I, []),
     "cernels_moe_decode_max_pairs": (_I, []),
     "cernels_moe_experts_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),

@@ -24,7 +24,7 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(PKG.parent / "include")]
 DEVICE = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-munsafe-fp-atomics"]
 
-SOURCES = ["moe_route.hip", "moe_gemm.hip", "moe_gemm_packed.hip", "moe_decode.hip", "moe_capi.cpp"]
+SOURCES = ["moe_route.hip", "moe_gemm.hip", "moe_gemm_packed.hip", "moe_decode.hip", "moe_router.hip", "moe_capi.cpp"]
 
 
 def _compile(src: str) -> Path:
@@ -41,7 +41,7 @@ def _compile(src: str) -> Path:
 
 def build(verbose: bool = False) -> Path:
     OBJ.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]

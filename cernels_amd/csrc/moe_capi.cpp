@@ -16,6 +16,10 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
 size_t route_workspace_bytes(int T, int K, int E);
 int gemm_tile_m();
 int packed_tile_m();
+int router_max_experts();
+int router_max_topk();
+hipError_t launch_router(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int T, int H, int E, int K,
+                         int mode, int renorm, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s);
 hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
@@ -142,6 +146,25 @@ int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, i
     if (workspace_bytes < cmoe::route_workspace_bytes(T, K, E)) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
     return hip_status(cmoe::launch_route(indices, T, K, E, tile_m, expert_offsets, sorted_pairs, tile_offsets,
                                          tile_expert, meta, static_cast<int32_t*>(workspace), stream));
+}
+
+int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,
+                       int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t* indices, float* weights,
+                       void* logits, hipStream_t stream) {
+    if (T < 0 || H <= 0 || E <= 0 || K <= 0) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (mode != CERNELS_MOE_ROUTER_SOFTMAX_TOPK && mode != CERNELS_MOE_ROUTER_TOPK_SOFTMAX)
+        return CERNELS_MOE_INVALID_ARGUMENT;
+    if (T == 0) return CERNELS_MOE_OK;
+    if (!x || !router_weight || !indices || !weights) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (K > E || K > cmoe::router_max_topk() || E > cmoe::router_max_experts() || H % 16)
+        return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (!aligned16(x) || !aligned16(router_weight)) return CERNELS_MOE_MISALIGNED;
+    if ((reinterpret_cast<uintptr_t>(router_bias) & 1u) || (reinterpret_cast<uintptr_t>(logits) & 1u) ||
+        (reinterpret_cast<uintptr_t>(indices) & 3u) || (reinterpret_cast<uintptr_t>(weights) & 3u))
+        return CERNELS_MOE_MISALIGNED;
+    return hip_status(cmoe::launch_router(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router_weight),
+                                          static_cast<const uint16_t*>(router_bias), T, H, E, K, mode, renorm != 0,
+                                          indices, weights, static_cast<uint16_t*>(logits), stream));
 }
 
 size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K) {

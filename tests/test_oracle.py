@@ -263,3 +263,66 @@ def test_eager_skips_out_of_range_ids():
     ref64 = O.experts_fp64(x, fixed, w2, W1, W2)
     assert O.error_stats(got, ref64)["ratio"] < 0.05
     torch.testing.assert_close(O.experts_fp64(x, bad, w, W1, W2), ref64, rtol=1e-14, atol=1e-14)
+
+
+# ---- router restatement -------------------------------------------------------------------------
+
+def _identity_router_inputs(T, E, seed, ties=False):
+    g = torch.Generator().manual_seed(seed)
+    if ties:
+        x = (torch.randint(-4, 5, (T, E), generator=g).float() * 0.25).bfloat16()
+    else:  # distinct values per row: a random permutation of an evenly spaced set
+        base = torch.linspace(-3.0, 3.0, E)
+        x = torch.stack([base[torch.randperm(E, generator=g)] for _ in range(T)]).bfloat16()
+        assert all(len(set(r.tolist())) == E for r in x.float())
+    return x
+
+
+@pytest.mark.parametrize("E,K", [(8, 2), (32, 4), (64, 10), (128, 8)])
+def test_router_select_matches_module_routers(E, K):
+    """With W = I (bf16 identity) the module routers' logits equal x exactly, so their own torch
+    code (topk / softmax / renorm) pins router_select on tie-free logits."""
+    from cernels_amd.configs.modules import GptOssRouter, Qwen3NextRouter
+
+    x = _identity_router_inputs(50, E, seed=E + K)
+    eye = torch.eye(E).bfloat16()
+    go = GptOssRouter(E, E, K)
+    q3 = Qwen3NextRouter(E, E, K, norm_topk_prob=True)
+    with torch.no_grad():
+        go.weight.copy_(eye)
+        q3.weight.copy_(eye)
+    go, q3 = go.bfloat16(), q3.bfloat16()
+    with torch.no_grad():
+        lg, sg, ig = go(x)
+        lq, sq, iq = q3(x)
+    assert torch.equal(lg, x) and torch.equal(lq, x)
+    idx, w = O.router_select(x, K, O.ROUTER_TOPK_SOFTMAX)
+    assert torch.equal(idx, ig) and torch.equal(w, sg)
+    idx, w = O.router_select(x, K, O.ROUTER_SOFTMAX_TOPK, renorm=True)
+    assert torch.equal(idx, iq) and torch.equal(w, sq)
+
+
+def test_router_select_closed_forms_and_ties():
+    x = _identity_router_inputs(20, 16, seed=3)
+    p = torch.softmax(x.float(), dim=-1)
+    # k = E: every expert, in descending order; weights are the softmax itself
+    for mode in (O.ROUTER_SOFTMAX_TOPK, O.ROUTER_TOPK_SOFTMAX):
+        idx, w = O.router_select(x, 16, mode, renorm=False)
+        assert torch.equal(torch.gather(p, 1, idx).bfloat16(), w)
+        assert torch.equal(idx.sort(dim=1).values, torch.arange(16).expand(20, 16))
+    # k = 1 renormalised: the argmax with weight exactly 1
+    idx, w = O.router_select(x, 1, O.ROUTER_SOFTMAX_TOPK, renorm=True)
+    assert torch.equal(idx[:, 0], x.float().argmax(dim=1)) and bool((w == 1).all())
+    # ties go to the lower expert id
+    t = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0]]).bfloat16()
+    idx, _ = O.router_select(t, 2, O.ROUTER_TOPK_SOFTMAX)
+    assert idx.tolist() == [[1, 2]]
+    idx, _ = O.router_select(t, 4, O.ROUTER_SOFTMAX_TOPK)
+    assert idx.tolist() == [[1, 2, 4, 3]]
+
+
+def test_router_logits_identity():
+    x = _identity_router_inputs(7, 24, seed=9, ties=True)
+    assert torch.equal(O.router_logits(x, torch.eye(24).bfloat16()), x)
+    b = torch.full((24,), 0.5).bfloat16()
+    assert torch.equal(O.router_logits(x, torch.eye(24).bfloat16(), b), (x.double() + 0.5).bfloat16())
