@@ -13,6 +13,11 @@ region and reported as ``pack_ms``. The same workload on the weights as stored (
 layout, ``cernels_moe_experts``) is timed beside it as ``native_layout``. Decode streams the
 weights as stored.
 
+For the gpt-oss and qwen3-next workloads, whose reference ops run the router inside the call, the
+fused router (``cernels_moe_router``, seeded router weights) is timed on its own as well and
+reported as ``router`` and ``op_ms_with_router``, beside the same router as torch ops (F.linear,
+softmax, topk: what the reference's loaders run) as ``router.torch_ops_ms``.
+
 Timing: W untimed warmup steps, then exactly K steps between two ``torch.cuda.synchronize()``;
 the step time is the HIP-event time of the K steps / K. Each step also records HIP events between
 its kernels on the launch stream, which gives each kernel's average duration (``stages``).
@@ -54,6 +59,9 @@ METRIC = "MoE experts prefill TFLOP/s + decode HBM GB/s (% roofline), 1 MI355X"
 COLD_BYTES = 1 << 30
 CAL_MIB = 256
 # kernel-name fragments of each stage's kernels in a rocprofv3 trace
+# workloads whose reference op call runs the router inside it (src/kops/registry/gpt_oss_moe_experts.py:35,
+# src/kops/registry/qwen3_next_moe_experts.py:28): the fused router is timed beside the experts op
+ROUTER_IN_OP = {"gpt_oss_20b_experts": ("topk_softmax", True), "qwen3_next_zipf": ("softmax_topk", False)}
 KERNEL_OF_STAGE = {
     "packed": {"gate_up": "moe_gemm_packed_kernel<0", "down": "moe_gemm_packed_kernel<1"},
     "native": {"gate_up": "moe_gemm_v3_kernel<0", "down": "moe_gemm_v3_kernel<1"},
@@ -105,6 +113,8 @@ def stage_model(shape, U, P, stage):
         return 2.0 * P * H * 2 * F, U * 2 * F * H * 2 + T * H * 2 + P * F * 2
     if stage == "decode_down":
         return 2.0 * P * F * H, U * H * F * 2 + P * F * 2 + T * H * 2
+    if stage == "router":  # x and the router weight (+ bias) read once, ids + fp32 weights written
+        return 2.0 * T * H * E, T * H * 2 + E * H * 2 + (E * 2 if shape.bias else 0) + P * 8
     raise KeyError(stage)
 
 
@@ -142,6 +152,33 @@ def _timed_steps(step, stages, steps, warmup, hip, stream):
                 for j, name in enumerate(stages)}
     ev.close()
     return ms, wall, stage_ms
+
+
+def _torch_router_ms(kind, x, w, b, k, steps, warmup):
+    """The reference's router as its transformers module computes it, in torch ops on the GPU
+    (GptOssTopKRouter modeling_gpt_oss.py:126-130, Qwen3NextTopKRouter modeling_qwen3_next.py:766-775)."""
+    import torch
+    import torch.nn.functional as F
+
+    def run():
+        logits = F.linear(x, w, b)
+        if kind == "topk_softmax":
+            v, i = torch.topk(logits, k, dim=-1)
+            return torch.softmax(v, dim=1, dtype=v.dtype), i
+        p = torch.softmax(logits, dtype=torch.float, dim=-1)
+        v, i = torch.topk(p, k, dim=-1)
+        return (v / v.sum(dim=-1, keepdim=True)).to(logits.dtype), i
+
+    for _ in range(warmup):
+        run()
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        run()
+    z.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(z) / steps
 
 
 def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
@@ -230,6 +267,26 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
 
             paths["native"] = _timed_steps(step_native, stages, steps, warmup, hip, stream)
 
+    router = None
+    if shape.name in ROUTER_IN_OP:
+        kind, with_bias = ROUTER_IN_OP[shape.name]
+        g = torch.Generator().manual_seed(7)
+        rw_w = (torch.randn(E, H, generator=g) * 0.02).bfloat16().to(dev)
+        rw_b = (torch.randn(E, generator=g) * 0.02).bfloat16().to(dev) if with_bias else None
+        r_idx = torch.empty((T, K), dtype=torch.int32, device=dev)
+        r_wt = torch.empty((T, K), dtype=torch.float32, device=dev)
+        r_lg = torch.empty((T, E), dtype=torch.bfloat16, device=dev)
+        mode = _native.ROUTER_TOPK_SOFTMAX if kind == "topk_softmax" else _native.ROUTER_SOFTMAX_TOPK
+
+        def step_router(i, ev_arr):
+            _native.check(L.cernels_moe_router(ptr(x), ptr(rw_w), ptr(rw_b), T, H, E, K, mode, 1, ptr(r_idx),
+                                               ptr(r_wt), ptr(r_lg), stream), "router")
+
+        rms, _, _ = _timed_steps(step_router, [], steps, warmup, hip, stream)
+        router = dict(ms=rms, mode=kind, **roofline_of(*stage_model(shape, U, P, "router"), rms))
+        router["torch_ms"] = _torch_router_ms(kind, x, rw_w, rw_b, K, steps, warmup)
+        del rw_w, rw_b, r_idx, r_wt, r_lg
+
     ms, wall, stage_ms = paths[main_path]
     flops = shape.flops()
     alg_bytes = touched + 2 * T * H * 2 + P * 8
@@ -245,6 +302,9 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
     )
     if pack_ms is not None:
         rec["pack_ms"] = pack_ms
+    if router is not None:
+        rec["router"] = router
+        rec["op_ms_with_router"] = ms + router["ms"]
     if "native" in paths:
         nms, _, nst = paths["native"]
         rec["native_layout"] = dict(ms=nms, tflops=flops / (nms * 1e-3) / 1e12, stages_ms=nst)
@@ -252,7 +312,10 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
         f"attainable {rec['attainable_frac'] * 100:.1f}%  stages " +
         " ".join(f"{k}={v['ms'] * 1e3:.1f}us" for k, v in rec["stages"].items()) +
         (f"  | native layout {rec['native_layout']['ms'] * 1e3:.1f}us" if "native_layout" in rec else "") +
-        (f"  | pack {pack_ms:.2f} ms once" if pack_ms is not None else ""))
+        (f"  | pack {pack_ms:.2f} ms once" if pack_ms is not None else "") +
+        (f"  | router {router['ms'] * 1e3:.1f}us ({router['frac'] * 100:.1f}% of {router['bound']} peak; "
+         f"torch ops {router['torch_ms'] * 1e3:.1f}us)"
+         if router is not None else ""))
     del W1, W2, ws, out
     torch.cuda.empty_cache()
     return rec
@@ -443,8 +506,12 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "per_config": {
-            n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items() if k not in ("stages", "native_layout")}
+            n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()
+                if k not in ("stages", "native_layout", "router")}
             | {"stages_ms": {s: round(v["ms"], 5) for s, v in r["stages"].items()}}
+            | ({"router": {"ms": round(r["router"]["ms"], 5), "mode": r["router"]["mode"], "bound": r["router"]["bound"],
+                           "frac": round(r["router"]["frac"], 4), "torch_ops_ms": round(r["router"]["torch_ms"], 5)}}
+               if "router" in r else {})
             | ({"native_layout_ms": round(r["native_layout"]["ms"], 5)} if "native_layout" in r else {})
             for n, r in per.items()
         },

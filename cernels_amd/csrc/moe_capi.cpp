@@ -155,7 +155,7 @@ int cernels_moe_router(const void* x, const void* router_weight, const void* rou
     if (mode != CERNELS_MOE_ROUTER_SOFTMAX_TOPK && mode != CERNELS_MOE_ROUTER_TOPK_SOFTMAX)
         return CERNELS_MOE_INVALID_ARGUMENT;
     if (T == 0) return CERNELS_MOE_OK;
-    if (!x || !router_weight || !indices || !weights) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (!x || !router_weight || !indices || !weights || !logits) return CERNELS_MOE_INVALID_ARGUMENT;
     if (K > E || K > cmoe::router_max_topk() || E > cmoe::router_max_experts() || H % 16)
         return CERNELS_MOE_UNSUPPORTED_SHAPE;
     if (!aligned16(x) || !aligned16(router_weight)) return CERNELS_MOE_MISALIGNED;

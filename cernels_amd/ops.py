@@ -196,7 +196,7 @@ def moe_router(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
                  and tuple(bias.shape) == (E,), "router bias must be bf16 [E] on x's device")
     idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
     wts = torch.empty((T, K), dtype=torch.float32, device=x.device)
-    logits = torch.empty((T, E), dtype=torch.bfloat16, device=x.device) if want_logits else None
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device=x.device)
     if T > 0:
         L = _native.lib()
         with torch.cuda.device(x.device):

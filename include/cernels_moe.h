@@ -152,11 +152,12 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
  *   CERNELS_MOE_ROUTER_TOPK_SOFTMAX: the K largest logits, softmax over those K values
  *       (transformers GptOssTopKRouter, modeling_gpt_oss.py:126-130).
  * Writes indices [T, K] int32 (descending by score; ties to the lower expert id) and weights [T, K]
- * fp32 holding the bf16-rounded scores, i.e. what the experts entries take. logits [T, E] bf16 is
- * optional (nullable). Replaces the module routers the reference's gpt-oss and qwen3 loaders call
- * inside their timed ops (src/kops/registry/gpt_oss_moe_experts.py:35,
+ * fp32 holding the bf16-rounded scores, i.e. what the experts entries take, and logits [T, E] bf16
+ * (required: the routers return them too, and for E > 64 they carry the logits from the GEMM kernel
+ * to the selection kernel). Replaces the module routers the reference's gpt-oss and qwen3 loaders
+ * call inside their timed ops (src/kops/registry/gpt_oss_moe_experts.py:35,
  * src/kops/registry/qwen3_next_moe_experts.py:28).
- * Limits: 1 <= K <= min(E, 32), E <= 1024, H % 16 == 0. */
+ * Limits: 1 <= K <= min(E, 32), E <= 1024, H % 16 == 0; x and W 16-byte aligned. */
 enum cernels_moe_router_mode { CERNELS_MOE_ROUTER_SOFTMAX_TOPK = 0, CERNELS_MOE_ROUTER_TOPK_SOFTMAX = 1 };
 int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,
                        int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t* indices, float* weights,

@@ -185,12 +185,16 @@ def router_select(logits, top_k: int, mode: int, renorm: bool = True):
 
     SOFTMAX_TOPK (modeling_qwen3_next.py:769-773): softmax in fp32, top-k, renormalise, bf16.
     TOPK_SOFTMAX (modeling_gpt_oss.py:128-129): top-k of the logits, softmax over them, bf16.
+    Both choose the experts on the logits: softmax is strictly increasing, so the top-k of the
+    probabilities is the top-k of the logits, and equal probabilities come only from equal logits.
+    (Choosing on fp32 probabilities instead would let the rounding of exp tie two distinct logits.)
     """
     lf = logits.float()
     if mode == ROUTER_SOFTMAX_TOPK:
         probs = torch.softmax(lf, dim=-1, dtype=torch.float32)
-        vals, order = torch.sort(probs, dim=-1, descending=True, stable=True)
-        w, idx = vals[:, :top_k], order[:, :top_k]
+        _, order = torch.sort(lf, dim=-1, descending=True, stable=True)
+        idx = order[:, :top_k]
+        w = torch.gather(probs, 1, idx)
         if renorm:
             w = w / w.sum(dim=-1, keepdim=True)
     elif mode == ROUTER_TOPK_SOFTMAX:

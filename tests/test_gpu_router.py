@@ -46,6 +46,11 @@ CASES = [
     (6, 70, 512, 1000, 16, O.ROUTER_SOFTMAX_TOPK, True, False),  # E not a multiple of 32
     (7, 5, 128, 32, 32, O.ROUTER_TOPK_SOFTMAX, True, True),  # k = E = the largest k
     (8, 64, 2048, 512, 1, O.ROUTER_SOFTMAX_TOPK, True, False),  # k = 1
+    (9, 129, 80, 48, 5, O.ROUTER_TOPK_SOFTMAX, True, True),  # H % 64 != 0, 32 < E <= 64 (fused)
+    (10, 257, 208, 96, 8, O.ROUTER_SOFTMAX_TOPK, False, True),  # H % 64 != 0, E > 64 (GEMM + select)
+    (11, 1, 2880, 32, 4, O.ROUTER_TOPK_SOFTMAX, True, True),  # gpt-oss decode
+    (12, 8, 2048, 512, 10, O.ROUTER_SOFTMAX_TOPK, True, False),  # qwen3-next decode
+    (13, 200, 128, 65, 3, O.ROUTER_TOPK_SOFTMAX, True, False),  # E = 65: smallest unfused
 ]
 
 

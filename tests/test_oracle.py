@@ -321,6 +321,20 @@ def test_router_select_closed_forms_and_ties():
     assert idx.tolist() == [[1, 2, 4, 3]]
 
 
+def test_router_select_orders_by_logit_where_fp32_probs_tie():
+    """Two distinct bf16 logits near zero whose fp32 softmax probabilities round equal: the expert
+    with the larger logit comes first (the exact probabilities differ), not the lower id."""
+    a, b = 2.0 ** -20, 2.0 ** -20 + 2.0 ** -27  # adjacent bf16 values
+    t = torch.tensor([[0.0, a, b, -1.0]]).bfloat16()
+    lo, hi = t[0, 1].item(), t[0, 2].item()
+    assert lo == a and hi == b and hi > lo
+    p = torch.softmax(t.float(), dim=-1)
+    assert p[0, 1] == p[0, 2]  # the fp32 probabilities tie
+    idx, w = O.router_select(t, 3, O.ROUTER_SOFTMAX_TOPK, renorm=False)
+    assert idx.tolist() == [[2, 1, 0]]  # the larger logit (id 2) before the lower id with the same fp32 probability
+    assert torch.equal(w, torch.gather(p, 1, idx).bfloat16())
+
+
 def test_router_logits_identity():
     x = _identity_router_inputs(7, 24, seed=9, ties=True)
     assert torch.equal(O.router_logits(x, torch.eye(24).bfloat16()), x)
