@@ -16,7 +16,9 @@ weights as stored.
 For the gpt-oss and qwen3-next workloads, whose reference ops run the router inside the call, the
 fused router (``cernels_moe_router``, seeded router weights) is timed on its own as well and
 reported as ``router`` and ``op_ms_with_router``, beside the same router as torch ops (F.linear,
-softmax, topk: what the reference's loaders run) as ``router.torch_ops_ms``.
+softmax, topk: what the reference's loaders run) as ``router.torch_ops_ms``. ``module_ops`` times the
+reference's module-level configs ``gpt_oss_moe_experts`` and ``qwen3_next_moe_experts`` through the
+drop-in loaders (router, and for qwen3 the gated shared expert, inside the call).
 
 Timing: W untimed warmup steps, then exactly K steps between two ``torch.cuda.synchronize()``;
 the step time is the HIP-event time of the K steps / K. Each step also records HIP events between
@@ -279,7 +281,7 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
         mode = _native.ROUTER_TOPK_SOFTMAX if kind == "topk_softmax" else _native.ROUTER_SOFTMAX_TOPK
 
         def step_router(i, ev_arr):
-            _native.check(L.cernels_moe_router(ptr(x), ptr(rw_w), ptr(rw_b), T, H, E, K, mode, 1, ptr(r_idx),
+            _native.check(L.cernels_moe_router(ptr(x), ptr(rw_w), ptr(rw_b), T, H, E, K, mode, 1, 0, ptr(r_idx),
                                                ptr(r_wt), ptr(r_lg), stream), "router")
 
         rms, _, _ = _timed_steps(step_router, [], steps, warmup, hip, stream)
@@ -317,6 +319,48 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
          f"torch ops {router['torch_ms'] * 1e3:.1f}us)"
          if router is not None else ""))
     del W1, W2, ws, out
+    torch.cuda.empty_cache()
+    return rec
+
+
+MODULE_OPS = ("gpt_oss_moe_experts", "qwen3_next_moe_experts")
+
+
+def run_module_op(name, steps, warmup, dev, log):
+    """The reference's module-level op as its config calls it (src/configs/registry/{gpt_oss,qwen3_next}_moe_experts.py):
+    the drop-in loader ``kernel(x, mlp)`` / ``kernel(x, block)`` with the router (and for qwen3 the gated
+    shared expert) inside the call, Python dispatch included, on seeded weights and near-uniform routing
+    as the reference's configs have it. Packing happens in the first warmup call."""
+    import torch
+
+    from cernels_amd.configs.registry import CONFIGS
+
+    cfg = CONFIGS[name]
+    t0 = time.time()
+    x, mod = cfg.inputs(dev)
+    log(f"[{name}] module inputs built in {time.time() - t0:.1f}s")
+    s = cfg.shape
+    T, H, F, E, K = s.tokens, s.hidden, s.ffn, s.experts, s.top_k
+    flops = 6.0 * T * K * H * F + 2.0 * T * H * E
+    shared_f = 0
+    if hasattr(mod, "shared_expert"):
+        shared_f = int(mod.shared_expert.gate_proj.weight.shape[0])
+        flops += 6.0 * T * H * shared_f + 2.0 * T * H
+    for _ in range(max(1, warmup)):
+        cfg.custom(x, mod)
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(steps):
+        cfg.custom(x, mod)
+    z.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(z) / steps
+    rec = dict(ms=ms, tflops=flops / (ms * 1e-3) / 1e12, tokens=T, hidden=H, ffn=F, experts=E, top_k=K,
+               shared_ffn=shared_f, flops=flops)
+    log(f"[{name}] module op (router{' + shared expert' if shared_f else ''} + experts): {ms:.4f} ms  "
+        f"{rec['tflops']:.1f} TFLOP/s")
+    del x, mod
     torch.cuda.empty_cache()
     return rec
 
@@ -426,11 +470,14 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--configs", default="all", help="'all', 'headline' or a comma list of BASELINE workload names")
+    ap.add_argument("--configs", default="all",
+                    help="'all', 'headline', 'module' (only the module-level loader ops) or a comma list of BASELINE "
+                         "workload names")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-native", action="store_true", help="skip timing prefill on the weights as stored")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE child runs")
+    ap.add_argument("--no-module-ops", action="store_true", help="skip the module-level gpt-oss / qwen3 loader timings")
     ap.add_argument("--inner-traffic", metavar="WORKLOAD", help=argparse.SUPPRESS)
     ap.add_argument("--report", default=str(ROOT / "gpurun_out" / "bench_report.json"))
     args = ap.parse_args()
@@ -456,6 +503,13 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     hip = _hip()
+    if args.configs == "module":
+        mods = {n: run_module_op(n, args.steps, args.warmup, dev, log) for n in MODULE_OPS}
+        print(json.dumps({"metric": "module-level MoE ops (drop-in loaders), ms per call", "unit": "ms",
+                          "higher_is_better": False, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "module_ops": {n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()}
+                                         for n, r in mods.items()}}), flush=True)
+        return
     if args.configs == "all":
         names = [HEADLINE] + [n for n in BASELINE_ORDER if n != HEADLINE]
     elif args.configs == "headline":
@@ -465,6 +519,10 @@ def main():
     per = {}
     for n in names:
         per[n] = run_config(BASELINE_SHAPES[n], args.steps, args.warmup, dev, hip, log, with_native=not args.no_native)
+    mods = {}
+    if not args.no_module_ops and args.configs == "all":
+        for n in MODULE_OPS:
+            mods[n] = run_module_op(n, args.steps, args.warmup, dev, log)
     head = per.get(HEADLINE) or per[names[0]]
     dom_name, dom = max(head["stages"].items(), key=lambda kv: kv[1]["ms"])
     traffic_mb = None
@@ -515,6 +573,7 @@ def main():
             | ({"native_layout_ms": round(r["native_layout"]["ms"], 5)} if "native_layout" in r else {})
             for n, r in per.items()
         },
+        "module_ops": {n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()} for n, r in mods.items()},
     }
     try:
         Path(args.report).parent.mkdir(parents=True, exist_ok=True)

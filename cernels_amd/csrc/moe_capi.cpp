@@ -19,7 +19,7 @@ int packed_tile_m();
 int router_max_experts();
 int router_max_topk();
 hipError_t launch_router(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int T, int H, int E, int K,
-                         int mode, int renorm, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s);
+                         int mode, int renorm, int S, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s);
 hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const void* w2, const float* b2,
                           const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K, int layout,
                           int act, void* out, int32_t* offsets, int32_t* tile_offsets, int32_t* meta,
@@ -85,8 +85,10 @@ DecodeWs decode_ws(int T, int H, int F, int K) {
     return w;
 }
 
+constexpr int kMaxTopk = 4096;  // the route kernels divide pair positions by T through a float reciprocal
+
 bool dims_ok(int T, int H, int F, int E, int K) {
-    return T >= 0 && H > 0 && F > 0 && E > 0 && K > 0 && (long long)T * K < (1LL << 31);
+    return T >= 0 && H > 0 && F > 0 && E > 0 && K > 0 && K <= kMaxTopk && (long long)T * K < (1LL << 31);
 }
 
 int common_checks(const void* x, const void* w1, const void* w2, const int32_t* idx, const float* wts, int T,
@@ -139,7 +141,7 @@ size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t 
 int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, int32_t tile_m,
                       int32_t* expert_offsets, int32_t* sorted_pairs, int32_t* tile_offsets, int32_t* tile_expert,
                       int32_t* meta, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (T < 0 || K <= 0 || E <= 0 || E > kMaxExperts || tile_m <= 0 || (long long)T * K >= (1LL << 31))
+    if (T < 0 || K <= 0 || K > kMaxTopk || E <= 0 || E > kMaxExperts || tile_m <= 0 || (long long)T * K >= (1LL << 31))
         return CERNELS_MOE_INVALID_ARGUMENT;
     if (!expert_offsets || !tile_offsets || !tile_expert || !meta || !workspace) return CERNELS_MOE_INVALID_ARGUMENT;
     if (T > 0 && (!indices || !sorted_pairs)) return CERNELS_MOE_INVALID_ARGUMENT;
@@ -149,14 +151,15 @@ int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, i
 }
 
 int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,
-                       int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t* indices, float* weights,
-                       void* logits, hipStream_t stream) {
-    if (T < 0 || H <= 0 || E <= 0 || K <= 0) return CERNELS_MOE_INVALID_ARGUMENT;
+                       int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t shared_slots, int32_t* indices,
+                       float* weights, void* logits, hipStream_t stream) {
+    if (T < 0 || H <= 0 || E <= 0 || K <= 0 || shared_slots < 0) return CERNELS_MOE_INVALID_ARGUMENT;
     if (mode != CERNELS_MOE_ROUTER_SOFTMAX_TOPK && mode != CERNELS_MOE_ROUTER_TOPK_SOFTMAX)
         return CERNELS_MOE_INVALID_ARGUMENT;
     if (T == 0) return CERNELS_MOE_OK;
     if (!x || !router_weight || !indices || !weights || !logits) return CERNELS_MOE_INVALID_ARGUMENT;
-    if (K > E || K > cmoe::router_max_topk() || E > cmoe::router_max_experts() || H % 16)
+    if (K > E || K > cmoe::router_max_topk() || shared_slots > cmoe::router_max_topk() ||
+        E + (shared_slots > 0) > cmoe::router_max_experts() || H % 16)
         return CERNELS_MOE_UNSUPPORTED_SHAPE;
     if (!aligned16(x) || !aligned16(router_weight)) return CERNELS_MOE_MISALIGNED;
     if ((reinterpret_cast<uintptr_t>(router_bias) & 1u) || (reinterpret_cast<uintptr_t>(logits) & 1u) ||
@@ -164,7 +167,7 @@ int cernels_moe_router(const void* x, const void* router_weight, const void* rou
         return CERNELS_MOE_MISALIGNED;
     return hip_status(cmoe::launch_router(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(router_weight),
                                           static_cast<const uint16_t*>(router_bias), T, H, E, K, mode, renorm != 0,
-                                          indices, weights, static_cast<uint16_t*>(logits), stream));
+                                          shared_slots, indices, weights, static_cast<uint16_t*>(logits), stream));
 }
 
 size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K) {

@@ -55,8 +55,17 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot, int* t
 constexpr int kRtTile = 1024;   // pairs per route tile
 constexpr int kRtThreads = 256; // 4 waves x 256 pairs
 
-__device__ __forceinline__ int expert_at(const int32_t* __restrict__ idx, int q, int T, int K, int E) {
-    const int k = q / T, t = q - k * T;
+// q / T for q = k*T + t with k < K <= 4096 (checked on the host): a float-reciprocal estimate is
+// within 3*2^-24 * k < 1 of q / T, so the truncated estimate is off by at most one and a single
+// exact integer correction fixes it. gfx950 has no integer divide; this replaces ~40 instructions.
+__device__ __forceinline__ int div_by_t(int q, int T, float rT) {
+    const int k = (int)((float)q * rT);
+    const int r = q - k * T;
+    return k + (r >= T ? 1 : 0) - (r < 0 ? 1 : 0);
+}
+
+__device__ __forceinline__ int expert_at(const int32_t* __restrict__ idx, int q, int T, int K, int E, float rT) {
+    const int k = div_by_t(q, T, rT), t = q - k * T;
     const int v = idx[t * K + k];
     return ((unsigned)v < (unsigned)E) ? v : -1;
 }
@@ -65,6 +74,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_count_kernel(const int32
                                                                        int E, int32_t* __restrict__ counts) {
     extern __shared__ int32_t h[];  // [E]
     const int tid = threadIdx.x, P = T * K;
+    const float rT = 1.0f / (float)T;
     for (int i = tid; i < E; i += kRtThreads) h[i] = 0;
     __syncthreads();
     const int q0 = blockIdx.x * kRtTile;
@@ -72,7 +82,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_count_kernel(const int32
     for (int j = tid; j < kRtTile; j += kRtThreads) {
         const int q = q0 + j;
         if (q < P) {
-            const int e = expert_at(idx, q, T, K, E);
+            const int e = expert_at(idx, q, T, K, E, rT);
             if (e >= 0) atomicAdd(&h[e], 1);
         }
     }
@@ -122,6 +132,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_scatter_kernel(const int
     extern __shared__ int32_t wh[];  // [4][E]: per-wave counts, then per-wave write cursors
     constexpr int kW = kRtThreads / kWave;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave, P = T * K;
+    const float rT = 1.0f / (float)T;
     const int q0 = blockIdx.x * kRtTile + w * (kRtTile / kW);
     const int q1 = min(P, q0 + kRtTile / kW);
     for (int i = tid; i < kW * E; i += kRtThreads) wh[i] = 0;
@@ -130,7 +141,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_scatter_kernel(const int
 #pragma unroll
     for (int c = 0; c < kRtTile / kW / kWave; ++c) {
         const int q = q0 + c * kWave + lane;
-        ex[c] = q < q1 ? expert_at(idx, q, T, K, E) : -1;
+        ex[c] = q < q1 ? expert_at(idx, q, T, K, E, rT) : -1;
         if (ex[c] >= 0) atomicAdd(&wh[w * E + ex[c]], 1);
     }
     __syncthreads();
@@ -183,22 +194,41 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ meta) {
     __shared__ int32_t h[kRtFusedCells];  // [ntiles][E]
-    __shared__ int32_t s_off[kRouteThreads];
     __shared__ int wave_tot[kRouteWaves];
-    const int tid = threadIdx.x, P = T * K;
+    const int tid = threadIdx.x, P = T * K;  // P <= kRtFusedCells * kRtTile here, far below 2^31
     for (int i = tid; i < ntiles * E; i += kRouteThreads) h[i] = 0;
     __syncthreads();
-    // Eight pairs per thread are loaded before any of their LDS atomics, so the loads overlap.
-    for (int q0 = tid; q0 < P; q0 += 8 * kRouteThreads) {
-        int ev[8];
+    // idx is read in memory order (pair i = t*K + k), four consecutive pairs per thread and chunk, so
+    // a wave's load touches 8 cache lines rather than one per lane; each pair is then counted in the
+    // tile of its slot-major position q = k*T + t. (t, k) of a chunk's first pair come from one
+    // exact division (double reciprocal: quotient < 2^31, error < 1, one correction), then k steps.
+    const double rK = 1.0 / (double)K;
+    const int nchunks = ceil_div(P, 4);
+    for (int c0 = tid; c0 < nchunks; c0 += 8 * kRouteThreads) {
+        int ev[8][4];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int q = q0 + u * kRouteThreads;
-            ev[u] = q < P ? expert_at(idx, q, T, K, E) : -1;
+            const int i = 4 * (c0 + u * kRouteThreads);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ev[u][v] = i + v < P ? idx[i + v] : -1;
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (ev[u] >= 0) atomicAdd(&h[((q0 + u * kRouteThreads) / kRtTile) * E + ev[u]], 1);
+        for (int u = 0; u < 8; ++u) {
+            const int i = 4 * (c0 + u * kRouteThreads);
+            if (i >= P) continue;
+            int t = (int)((double)i * rK), k = i - t * K;
+            t += (k >= K ? 1 : 0) - (k < 0 ? 1 : 0);
+            k = i - t * K;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int e = ev[u][v];
+                if ((unsigned)e < (unsigned)E) atomicAdd(&h[((k * T + t) / kRtTile) * E + e], 1);
+                if (++k == K) {
+                    k = 0;
+                    ++t;
+                }
+            }
+        }
     }
     __syncthreads();
     const int e = tid;  // E <= kRouteThreads is checked on the host
@@ -217,11 +247,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     if (e < E) {
         offsets[e] = off;
         tile_offsets[e] = toff;
-        s_off[e] = off;
         for (int j = 0; j < nt; ++j) tile_expert[toff + j] = e;
+        for (int t = 0; t < ntiles; ++t) counts[t * E + e] = h[t * E + e] + off;  // absolute positions
     }
-    __syncthreads();  // every expert's prefix over tiles is in h, its offset in s_off
-    for (int i = tid; i < ntiles * E; i += kRouteThreads) counts[i] = h[i] + s_off[i % E];  // absolute positions
     if (tid == 0) {
         offsets[E] = valid_total;
         tile_offsets[E] = tiles_total;

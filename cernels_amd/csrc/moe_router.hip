@@ -103,13 +103,16 @@ __device__ __forceinline__ void sort_desc(uint32_t (&a)[N]) {
 }
 
 // Selection for token t by one wave (all 64 lanes active). v[j] = bf16 logit of expert lane + 64 j.
+// Output row t has K + S slots: the K chosen experts, then S shared-expert slots with ids E..E+S-1
+// and weight bf16(sigmoid(gate_logit)) (the Qwen3-Next shared-expert gate, modeling_qwen3_next.py:794).
 // The experts are chosen on the logits in both modes: softmax is strictly increasing, so the top-k
 // of the probabilities is the top-k of the logits, and equal probabilities come only from equal
 // logits. Each lane sorts its keys; round k takes the wave-wide maximum of the lanes' heads and the
 // lane holding it pops its head. Lane k keeps the k-th key.
 template <int MODE, int EJ>
 __device__ __forceinline__ void select_token(const float (&v)[EJ], int lane, long long t, int E, int K, int renorm,
-                                             int32_t* __restrict__ idx_out, float* __restrict__ w_out) {
+                                             int S, float gate_logit, int32_t* __restrict__ idx_out,
+                                             float* __restrict__ w_out) {
     uint32_t key[EJ];
 #pragma unroll
     for (int j = 0; j < EJ; ++j) key[j] = lane + kWave * j < E ? order_key(v[j], lane + kWave * j) : 0u;
@@ -139,9 +142,13 @@ __device__ __forceinline__ void select_token(const float (&v)[EJ], int lane, lon
         const float ex = lane < K ? __expf(lsel - lmax) : 0.f;
         wt = ex / wave_sum_f32(ex);
     }
+    const int KO = K + S;
     if (lane < K) {
-        idx_out[t * K + lane] = key_expert(sel);
-        w_out[t * K + lane] = round_bf16(wt);
+        idx_out[t * KO + lane] = key_expert(sel);
+        w_out[t * KO + lane] = round_bf16(wt);
+    } else if (lane < KO) {
+        idx_out[t * KO + lane] = E + lane - K;
+        w_out[t * KO + lane] = round_bf16(1.f / (1.f + __expf(-gate_logit)));
     }
 }
 
@@ -210,9 +217,10 @@ constexpr int kRtrFusedStages = 8;
 template <int MODE, int NT>  // NT = expert blocks of 32 (1 or 2)
 __global__ __launch_bounds__(kRtrThreads) void moe_router_fused_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias, int T, int H,
-    int E, int K, int renorm, int32_t* __restrict__ idx_out, float* __restrict__ w_out,
+    int E, int K, int renorm, int S, int32_t* __restrict__ idx_out, float* __restrict__ w_out,
     uint16_t* __restrict__ logits_out) {
     constexpr int TM = 32, EN = 32 * NT, ROWS = TM + EN;
+    const int ER = E + (S > 0);  // rows of W and of a logits row: the experts, then the shared-expert gate
     constexpr int kRing = kRtrFusedStages * ROWS * kBK * 2;
     static_assert(4 * TM * EN * 4 <= kRing, "partial sums reuse the stage ring");
     __shared__ __align__(1024) char ring[kRing];
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(kRtrThreads) void moe_router_fused_kernel(
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
     // wave q takes k-step q of every stage; a k-step at or beyond H is skipped
-    stage_pipeline<kRtrFusedStages, ROWS, TM>(ring, x, w, t0, 0, T, E, H, wave, lane, [&](const char* sb, int st) {
+    stage_pipeline<kRtrFusedStages, ROWS, TM>(ring, x, w, t0, 0, T, ER, H, wave, lane, [&](const char* sb, int st) {
         if (st * kBK + 16 * wave < H) {
             const bf16x8 a = lds_frag(sb, 0, wave, lane);
 #pragma unroll
@@ -244,26 +252,27 @@ __global__ __launch_bounds__(kRtrThreads) void moe_router_fused_kernel(
     // logit = bf16(((p0 + p1) + p2) + p3 + b); kept in slice 0 and written to logits_out
     for (int c = tid; c < TM * EN; c += kRtrThreads) {
         const int tl = c / EN, e = c % EN;
-        if (e >= E) continue;
+        if (e >= ER) continue;
         const float b = bias != nullptr ? bf16_bits_to_f32(bias[e]) : 0.f;
         const float v = round_bf16(((part[0][tl][e] + part[1][tl][e]) + part[2][tl][e]) + part[3][tl][e] + b);
         part[0][tl][e] = v;
-        if (t0 + tl < T) logits_out[(long long)(t0 + tl) * E + e] = f32_to_bf16_bits(v);
+        if (t0 + tl < T) logits_out[(long long)(t0 + tl) * ER + e] = f32_to_bf16_bits(v);
     }
     __syncthreads();
     for (int tl = wave; tl < TM; tl += 4) {
         if (t0 + tl >= T) break;  // uniform
         float v[1] = {lane < E ? part[0][tl][lane] : -INFINITY};
-        select_token<MODE, 1>(v, lane, t0 + tl, E, K, renorm, idx_out, w_out);
+        select_token<MODE, 1>(v, lane, t0 + tl, E, K, renorm, S, S > 0 ? part[0][tl][E] : 0.f, idx_out, w_out);
     }
 }
 
-// ---- E > 64: tiled logits GEMM, 128 tokens x 64 experts per workgroup; grid = (ceil(T/128), ceil(E/64))
+// ---- E > 64: tiled logits GEMM, 128 tokens x 64 experts per workgroup; grid = (ceil(T/128), ceil(E/64));
+// logits rows are ldl apart (E + 1 with a shared-expert gate, whose logit the selection kernel adds)
 constexpr int kRtrTiledStages = 4;
 __global__ __launch_bounds__(kRtrThreads) void moe_router_logits_kernel(const uint16_t* __restrict__ x,
                                                                         const uint16_t* __restrict__ w,
                                                                         const uint16_t* __restrict__ bias, int T,
-                                                                        int H, int E,
+                                                                        int H, int E, int ldl,
                                                                         uint16_t* __restrict__ logits_out) {
     constexpr int TM = 128, EN = 64, ROWS = TM + EN;
     __shared__ __align__(1024) char ring[kRtrTiledStages * ROWS * kBK * 2];
@@ -303,28 +312,47 @@ __global__ __launch_bounds__(kRtrThreads) void moe_router_logits_kernel(const ui
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int t = t0 + 32 * wave + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (t < T) logits_out[(long long)t * E + e] = f32_to_bf16_bits(acc[n][r] + b);
+            if (t < T) logits_out[(long long)t * ldl + e] = f32_to_bf16_bits(acc[n][r] + b);
         }
     }
 }
 
 // ---- E > 64: selection from the bf16 logits, one wave per token; grid = ceil(T / 4)
+// With S > 0 the wave also computes the shared-expert gate logit, bf16(x_t . w_E (+ b_E)), as a dot
+// product over H (16 bf16 per lane per step, fp32, DPP sum) and stores it in logits column E.
 template <int MODE, int EJ>  // EJ = experts per lane = ceil(E / 64)
-__global__ __launch_bounds__(kRtrThreads) void moe_router_select_kernel(const uint16_t* __restrict__ logits, int T,
-                                                                        int E, int K, int renorm,
-                                                                        int32_t* __restrict__ idx_out,
-                                                                        float* __restrict__ w_out) {
+__global__ __launch_bounds__(kRtrThreads) void moe_router_select_kernel(
+    uint16_t* __restrict__ logits, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ bias, int T, int H, int E, int K, int renorm, int S, int32_t* __restrict__ idx_out,
+    float* __restrict__ w_out) {
     const int lane = threadIdx.x & (kWave - 1);
     const int t = blockIdx.x * 4 + (int)(threadIdx.x / kWave);
     if (t >= T) return;  // uniform per wave
-    const uint16_t* row = logits + (long long)t * E;
+    uint16_t* row = logits + (long long)t * (E + (S > 0));
+    float gate = 0.f;
+    if (S > 0) {
+        const uint16_t* xr = x + (long long)t * H;
+        const uint16_t* gr = w + (long long)E * H;
+        float acc = 0.f;
+        for (int h = 8 * lane; h < H; h += 8 * kWave) {  // H % 16 == 0: whole 8-element chunks
+            const u32x4 xa = *reinterpret_cast<const u32x4*>(xr + h);
+            const u32x4 ga = *reinterpret_cast<const u32x4*>(gr + h);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc = fmaf(__uint_as_float(xa[q] << 16), __uint_as_float(ga[q] << 16), acc);
+                acc = fmaf(__uint_as_float(xa[q] & 0xffff0000u), __uint_as_float(ga[q] & 0xffff0000u), acc);
+            }
+        }
+        gate = round_bf16(wave_sum_f32(acc) + (bias != nullptr ? bf16_bits_to_f32(bias[E]) : 0.f));
+        if (lane == 0) row[E] = f32_to_bf16_bits(gate);
+    }
     float v[EJ];
 #pragma unroll
     for (int j = 0; j < EJ; ++j) {
         const int e = lane + kWave * j;
         v[j] = e < E ? bf16_bits_to_f32(row[e]) : -INFINITY;
     }
-    select_token<MODE, EJ>(v, lane, t, E, K, renorm, idx_out, w_out);
+    select_token<MODE, EJ>(v, lane, t, E, K, renorm, S, gate, idx_out, w_out);
 }
 
 int router_max_experts() { return kRtrMaxE; }
@@ -332,24 +360,25 @@ int router_max_topk() { return kRtrMaxK; }
 
 template <int MODE>
 static hipError_t launch_router_m(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int T, int H, int E,
-                                  int K, int renorm, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s) {
-    if (E <= kRtrFusedMaxE) {
+                                  int K, int renorm, int S, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s) {
+    const int ER = E + (S > 0);
+    if (ER <= kRtrFusedMaxE) {
         const dim3 grid(ceil_div(T, 32));
-        if (E <= 32)
+        if (ER <= 32)
             hipLaunchKernelGGL((moe_router_fused_kernel<MODE, 1>), grid, dim3(kRtrThreads), 0, s, x, w, bias, T, H, E,
-                               K, renorm, idx, wt, logits);
+                               K, renorm, S, idx, wt, logits);
         else
             hipLaunchKernelGGL((moe_router_fused_kernel<MODE, 2>), grid, dim3(kRtrThreads), 0, s, x, w, bias, T, H, E,
-                               K, renorm, idx, wt, logits);
+                               K, renorm, S, idx, wt, logits);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(moe_router_logits_kernel, dim3(ceil_div(T, 128), ceil_div(E, 64)), dim3(kRtrThreads), 0, s, x,
-                       w, bias, T, H, E, logits);
+    hipLaunchKernelGGL(moe_router_logits_kernel, dim3(ceil_div(T, 128), ceil_div(E, 64)), dim3(kRtrThreads), 0, s,
+                       x, w, bias, T, H, E, ER, logits);
     const dim3 grid(ceil_div(T, 4));
     const int ej = ceil_div(E, kWave);
 #define CMOE_RTR(EJ) \
-    hipLaunchKernelGGL((moe_router_select_kernel<MODE, EJ>), grid, dim3(kRtrThreads), 0, s, logits, T, E, K, renorm, \
-                       idx, wt)
+    hipLaunchKernelGGL((moe_router_select_kernel<MODE, EJ>), grid, dim3(kRtrThreads), 0, s, logits, x, w, bias, T, H, \
+                       E, K, renorm, S, idx, wt)
     if (ej <= 2) CMOE_RTR(2);
     else if (ej <= 4) CMOE_RTR(4);
     else if (ej <= 8) CMOE_RTR(8);
@@ -358,12 +387,14 @@ static hipError_t launch_router_m(const uint16_t* x, const uint16_t* w, const ui
     return hipGetLastError();
 }
 
-// Shapes were checked by the caller: 1 <= K <= min(E, 32), E <= 1024, H % 16 == 0, T >= 1, logits
-// non-null ([T, E] bf16).
+// Shapes were checked by the caller: 1 <= K <= min(E, 32), 0 <= S <= 32, E + (S > 0) <= 1024,
+// H % 16 == 0, T >= 1; W and bias have E + (S > 0) rows, logits is [T, E + (S > 0)] bf16, ids and
+// weights are [T, K + S].
 hipError_t launch_router(const uint16_t* x, const uint16_t* w, const uint16_t* bias, int T, int H, int E, int K,
-                         int mode, int renorm, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s) {
-    if (mode == kRouterSoftmaxTopk) return launch_router_m<kRouterSoftmaxTopk>(x, w, bias, T, H, E, K, renorm, idx, wt, logits, s);
-    return launch_router_m<kRouterTopkSoftmax>(x, w, bias, T, H, E, K, renorm, idx, wt, logits, s);
+                         int mode, int renorm, int S, int32_t* idx, float* wt, uint16_t* logits, hipStream_t s) {
+    if (mode == kRouterSoftmaxTopk)
+        return launch_router_m<kRouterSoftmaxTopk>(x, w, bias, T, H, E, K, renorm, S, idx, wt, logits, s);
+    return launch_router_m<kRouterTopkSoftmax>(x, w, bias, T, H, E, K, renorm, S, idx, wt, logits, s);
 }
 
 }  // namespace cmoe

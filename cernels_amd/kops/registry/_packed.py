@@ -23,10 +23,11 @@ def _key(params):
     return tuple(None if p is None else (p.data_ptr(), p._version, tuple(p.shape), str(p.device)) for p in params)
 
 
-def invalidate(experts) -> None:
-    """Forget the packed copy (needed after writes through ``param.data``)."""
-    if hasattr(experts, _ATTR):
-        delattr(experts, _ATTR)
+def invalidate(module) -> None:
+    """Forget the packed copies (needed after writes through ``param.data``)."""
+    for attr in (_ATTR, "_cernels_packed_block"):
+        if hasattr(module, attr):
+            delattr(module, attr)
 
 
 def packed_experts(experts, *, layout=ops.LAYOUT_CONCAT, act=ops.ACT_SILU, with_bias=False):
@@ -42,3 +43,31 @@ def packed_experts(experts, *, layout=ops.LAYOUT_CONCAT, act=ops.ACT_SILU, with_
                               down_bias=b2)
     setattr(experts, _ATTR, (key, pk))
     return pk
+
+
+_BLOCK_ATTR = "_cernels_packed_block"
+
+
+def packed_block(block):
+    """Qwen3-Next block: (packed routed + shared experts, router weight [E+1, H], shared slots S).
+
+    The router weight gets the shared-expert gate (``shared_expert_gate.weight``, [1, H]) as its last
+    row, so the fused router computes the gate logit with the routing logits. Cached on the block
+    with the same keying as ``packed_experts`` (every source tensor of the block).
+    """
+    e, sh = block.experts, block.shared_expert
+    params = (e.gate_up_proj, e.down_proj, sh.gate_proj.weight, sh.up_proj.weight, sh.down_proj.weight,
+              block.gate.weight, block.shared_expert_gate.weight)
+    key = _key(params)
+    cached = getattr(block, _BLOCK_ATTR, None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    if getattr(block.shared_expert_gate, "bias", None) is not None:
+        raise RuntimeError("shared_expert_gate with a bias is not supported (Qwen3-Next has none)")
+    with torch.no_grad():
+        pk, S = ops.pack_experts_with_shared(e.gate_up_proj.data, e.down_proj.data, sh.gate_proj.weight.data,
+                                             sh.up_proj.weight.data, sh.down_proj.weight.data)
+        rw = torch.cat([block.gate.weight.data, block.shared_expert_gate.weight.data], dim=0).contiguous()
+    val = (pk, rw, S)
+    setattr(block, _BLOCK_ATTR, (key, val))
+    return val

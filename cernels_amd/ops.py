@@ -121,19 +121,65 @@ class PackedExperts:
         self.gate_up_bias, self.down_bias = gate_up_bias, down_bias
 
 
-def pack_weights(weight: torch.Tensor, layout: int, which: int, H: int, F: int) -> torch.Tensor:
-    """One projection of every expert, packed by cernels_moe_pack_weights (runs on weight's stream)."""
+def pack_weights(weight: torch.Tensor, layout: int, which: int, H: int, F: int,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """One projection of every expert, packed by cernels_moe_pack_weights (runs on weight's stream).
+
+    Each expert's packed block is contiguous and expert-major, so packing experts [0, a) and [a, b)
+    into consecutive slices of one buffer equals packing [0, b) at once (``out`` is such a slice).
+    """
     _require(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.dim() == 3,
              "weight must be a contiguous bf16 CUDA tensor [E, ., .]")
     E = int(weight.size(0))
     L = _native.lib()
     nbytes = L.cernels_moe_packed_weight_bytes(H, F, E, which)
     _require(nbytes > 0 and nbytes == weight.numel() * 2, f"cannot pack H={H} F={F} (need H % 64 == 0, F % 64 == 0)")
-    out = torch.empty(weight.numel(), dtype=torch.bfloat16, device=weight.device)
+    if out is None:
+        out = torch.empty(weight.numel(), dtype=torch.bfloat16, device=weight.device)
+    _require(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == weight.numel()
+             and out.device == weight.device, "out must be a contiguous bf16 buffer of the weight's size")
     with torch.cuda.device(weight.device):
         st = L.cernels_moe_pack_weights(_ptr(weight), H, F, E, layout, which, _ptr(out), _stream(weight.device))
     check(st, "cernels_moe_pack_weights")
     return out
+
+
+def split_shared_expert(shared_gate, shared_up, shared_down, F: int):
+    """A dense SwiGLU MLP (gate/up [F_s, H], down [H, F_s]) as S = ceil(F_s/F) experts of width F in
+    the concat layout: (gate_up [S, 2F, H], down [S, H, F]). Block i holds intermediate columns
+    iF..iF+F-1; the last block is zero-padded, which adds silu(0)·0 = 0. Summing the S experts'
+    outputs gives the MLP's output."""
+    Fs, H = map(int, shared_gate.shape)
+    _require(tuple(shared_up.shape) == (Fs, H) and tuple(shared_down.shape) == (H, Fs), "shared expert shapes")
+    S = -(-Fs // F)
+    pad = S * F - Fs
+    g = torch.nn.functional.pad(shared_gate, (0, 0, 0, pad)).reshape(S, F, H)
+    u = torch.nn.functional.pad(shared_up, (0, 0, 0, pad)).reshape(S, F, H)
+    gu = torch.cat([g, u], dim=1).contiguous()
+    dn = torch.nn.functional.pad(shared_down, (0, pad)).reshape(H, S, F).permute(1, 0, 2).contiguous()
+    return gu, dn
+
+
+def pack_experts_with_shared(gate_up_proj, down_proj, shared_gate, shared_up, shared_down) -> tuple[PackedExperts, int]:
+    """Routed experts (concat layout, no biases) plus a dense SwiGLU shared expert, packed as one set.
+
+    The shared expert ``down(silu(gate x) * up x)`` with intermediate size F_s becomes S = ceil(F_s/F)
+    experts E..E+S-1 of width F: its gate/up rows and down columns are cut into S blocks, the last
+    zero-padded (silu(0)·0 = 0, so padding adds nothing). The sum over the S blocks is the shared
+    expert's output, so routing every token to E..E+S-1 with weight sigmoid(x·g) adds the gated
+    shared expert (modeling_qwen3_next.py:789-795). Returns (packed, S).
+    """
+    E, F2, H = map(int, gate_up_proj.shape)
+    F = F2 // 2
+    sgu, sdn = split_shared_expert(shared_gate, shared_up, shared_down, F)
+    S = int(sgu.shape[0])
+    gu = torch.empty(gate_up_proj.numel() + sgu.numel(), dtype=torch.bfloat16, device=gate_up_proj.device)
+    dn = torch.empty(down_proj.numel() + sdn.numel(), dtype=torch.bfloat16, device=down_proj.device)
+    pack_weights(gate_up_proj.contiguous(), LAYOUT_CONCAT, _native.GATE_UP, H, F, out=gu[:gate_up_proj.numel()])
+    pack_weights(sgu, LAYOUT_CONCAT, _native.GATE_UP, H, F, out=gu[gate_up_proj.numel():])
+    pack_weights(down_proj.contiguous(), LAYOUT_CONCAT, _native.DOWN, H, F, out=dn[:down_proj.numel()])
+    pack_weights(sdn, LAYOUT_CONCAT, _native.DOWN, H, F, out=dn[down_proj.numel():])
+    return PackedExperts(gu, dn, H, F, E + S, ACT_SILU, LAYOUT_CONCAT), S
 
 
 def pack_experts(gate_up_proj, down_proj, *, layout=LAYOUT_CONCAT, act=ACT_SILU, gate_up_bias=None,
@@ -177,30 +223,34 @@ def moe_experts_packed(x: torch.Tensor, packed: PackedExperts, indices: torch.Te
 
 
 def moe_router(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, top_k: int, mode: int,
-               renorm: bool = True, want_logits: bool = False):
-    """Fused router: (indices [T,K] int32, weights [T,K] float32[, logits [T,E] bf16]).
+               renorm: bool = True, want_logits: bool = False, shared_slots: int = 0):
+    """Fused router: (indices [T,K+S] int32, weights [T,K+S] float32[, logits [T,E'] bf16]).
 
     mode ROUTER_SOFTMAX_TOPK: softmax over bf16 logits in fp32, top-k, renormalised if ``renorm``
     (Qwen3NextTopKRouter); ROUTER_TOPK_SOFTMAX: top-k of the logits, softmax over the k values
     (GptOssTopKRouter). Weights are the bf16-rounded scores as float32; ties go to the lower id.
+    ``shared_slots`` S > 0: the last row of ``weight`` is the shared-expert gate (E' = E + 1 rows);
+    every token gets S more slots with ids E..E+S-1 and weight bf16(sigmoid(x · gate)).
     """
     _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2, "x must be bf16 [T, H]")
     _require(weight.device == x.device and weight.dtype == torch.bfloat16 and weight.is_contiguous()
              and weight.dim() == 2, "router weight must be bf16 [E, H] on x's device")
     T, H = map(int, x.shape)
-    E = int(weight.shape[0])
+    S = int(shared_slots)
+    ER = int(weight.shape[0])
+    E = ER - (1 if S > 0 else 0)
     K = int(top_k)
-    _require(int(weight.shape[1]) == H, "router weight shape mismatch")
+    _require(int(weight.shape[1]) == H and E >= 1, "router weight shape mismatch")
     if bias is not None:
         _require(bias.device == x.device and bias.dtype == torch.bfloat16 and bias.is_contiguous()
-                 and tuple(bias.shape) == (E,), "router bias must be bf16 [E] on x's device")
-    idx = torch.empty((T, K), dtype=torch.int32, device=x.device)
-    wts = torch.empty((T, K), dtype=torch.float32, device=x.device)
-    logits = torch.empty((T, E), dtype=torch.bfloat16, device=x.device)
+                 and tuple(bias.shape) == (ER,), "router bias must be bf16 [E'] on x's device")
+    idx = torch.empty((T, K + S), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, K + S), dtype=torch.float32, device=x.device)
+    logits = torch.empty((T, ER), dtype=torch.bfloat16, device=x.device)
     if T > 0:
         L = _native.lib()
         with torch.cuda.device(x.device):
-            st = L.cernels_moe_router(_ptr(x), _ptr(weight), _ptr(bias), T, H, E, K, int(mode), int(bool(renorm)),
+            st = L.cernels_moe_router(_ptr(x), _ptr(weight), _ptr(bias), T, H, E, K, int(mode), int(bool(renorm)), S,
                                       _ptr(idx), _ptr(wts), _ptr(logits), _stream(x.device))
         check(st, "cernels_moe_router")
     return (idx, wts, logits) if want_logits else (idx, wts)

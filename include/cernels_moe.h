@@ -66,7 +66,7 @@ const char* cernels_moe_status_string(int status);
  *   tile_expert    [cernels_moe_route_tile_capacity()]: expert of each M-tile.
  *   meta           [2]  : meta[0] = number of M-tiles, meta[1] = valid pairs.
  *   workspace      scratch of cernels_moe_route_workspace_bytes() (per-tile expert counts).
- * Limits: 1 <= E <= 1024, T*K < 2^31, tile_m >= 1. */
+ * Limits: 1 <= E <= 1024, 1 <= K <= 4096, T*K < 2^31, tile_m >= 1. */
 size_t cernels_moe_route_tile_capacity(int32_t T, int32_t K, int32_t E, int32_t tile_m);
 size_t cernels_moe_route_workspace_bytes(int32_t T, int32_t K, int32_t E);
 int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, int32_t tile_m,
@@ -77,7 +77,7 @@ int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, i
 /* ---- prefill: grouped GEMM experts ------------------------------------------------------------
  * route -> gate_up GEMM (+bias, SwiGLU in the epilogue) -> down GEMM (+bias, x routing weight in
  * the epilogue) -> deterministic top-k combine. Any T >= 0 (T = 0 is a no-op).
- * Limits: H % 64 == 0, F % 64 == 0, E <= 1024. */
+ * Limits: H % 64 == 0, F % 64 == 0, E <= 1024, K <= 4096. */
 size_t cernels_moe_experts_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t K);
 int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* gate_up_bias,
                         const void* down_proj, const float* down_bias, const int32_t* indices,
@@ -107,7 +107,7 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
  *          (src [E,H,F] concat or [E,F,H] interleaved).
  *   bias_layout (experts_packed): column order of gate_up_bias, CERNELS_MOE_LAYOUT_CONCAT
  *          ([gate F | up F]) or CERNELS_MOE_LAYOUT_INTERLEAVED (gate/up alternating).
- * Limits: H % 64 == 0, F % 64 == 0, E <= 1024; experts_packed also T*H*2 < 2^31 (32-bit offsets).
+ * Limits: H % 64 == 0, F % 64 == 0, E <= 1024, K <= 4096; experts_packed also T*H*2 < 2^31 (32-bit offsets).
  * Otherwise CERNELS_MOE_UNSUPPORTED_SHAPE. */
 size_t cernels_moe_packed_weight_bytes(int32_t H, int32_t F, int32_t E, int32_t which);
 int cernels_moe_pack_weights(const void* src, int32_t H, int32_t F, int32_t E, int32_t layout, int32_t which,
@@ -151,17 +151,22 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
  *       modeling_qwen3_next.py:766-775);
  *   CERNELS_MOE_ROUTER_TOPK_SOFTMAX: the K largest logits, softmax over those K values
  *       (transformers GptOssTopKRouter, modeling_gpt_oss.py:126-130).
- * Writes indices [T, K] int32 (descending by score; ties to the lower expert id) and weights [T, K]
- * fp32 holding the bf16-rounded scores, i.e. what the experts entries take, and logits [T, E] bf16
- * (required: the routers return them too, and for E > 64 they carry the logits from the GEMM kernel
- * to the selection kernel). Replaces the module routers the reference's gpt-oss and qwen3 loaders
- * call inside their timed ops (src/kops/registry/gpt_oss_moe_experts.py:35,
+ * Writes indices [T, K+S] int32 (descending by score; ties to the lower expert id) and weights
+ * [T, K+S] fp32 holding the bf16-rounded scores, i.e. what the experts entries take, and logits
+ * [T, E'] bf16 (required: the routers return them too, and for E' > 64 they carry the logits from the
+ * GEMM kernel to the selection kernel). Replaces the module routers the reference's gpt-oss and qwen3
+ * loaders call inside their timed ops (src/kops/registry/gpt_oss_moe_experts.py:35,
  * src/kops/registry/qwen3_next_moe_experts.py:28).
- * Limits: 1 <= K <= min(E, 32), E <= 1024, H % 16 == 0; x and W 16-byte aligned. */
+ * Shared expert (shared_slots = S > 0, Qwen3NextSparseMoeBlock, modeling_qwen3_next.py:789-795): W and
+ * b have E' = E + 1 rows, the last being shared_expert_gate's weight; slots K..K+S-1 of every token get
+ * ids E..E+S-1 and weight bf16(sigmoid(logit E)). With the shared expert's MLP packed as experts
+ * E..E+S-1 (its intermediate split into S blocks of F), the experts op then adds
+ * sigmoid(x g) * shared_expert(x) to the routed sum. S = 0: E' = E and K slots.
+ * Limits: 1 <= K <= min(E, 32), 0 <= S <= 32, E' <= 1024, H % 16 == 0; x and W 16-byte aligned. */
 enum cernels_moe_router_mode { CERNELS_MOE_ROUTER_SOFTMAX_TOPK = 0, CERNELS_MOE_ROUTER_TOPK_SOFTMAX = 1 };
 int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,
-                       int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t* indices, float* weights,
-                       void* logits, hipStream_t stream);
+                       int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t shared_slots, int32_t* indices,
+                       float* weights, void* logits, hipStream_t stream);
 
 /* ---- the reference's per-model ops, same argument order as their torch schemas ----------------
  * cohere2_moe_experts(Tensor x, Tensor gate_up_proj, Tensor down_proj, Tensor indices,

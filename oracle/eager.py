@@ -206,6 +206,20 @@ def router_select(logits, top_k: int, mode: int, renorm: bool = True):
     return idx, w.to(torch.bfloat16)
 
 
+def shared_expert_fp64(x, gate_proj, up_proj, down_proj, shared_gate):
+    """``sigmoid(shared_expert_gate(x)) * shared_expert(x)`` of Qwen3NextSparseMoeBlock
+    (transformers/models/qwen3_next/modeling_qwen3_next.py:789-795, Qwen3NextMLP :730-745 style
+    ``down(silu(gate x) * up x)``). The gate logit and its sigmoid are rounded to bf16, as the bf16
+    ``nn.Linear`` and ``torch.sigmoid`` produce them; the MLP is float64 with no intermediate
+    rounding. Returns fp64 [T, H]."""
+    d = torch.float64
+    xd = x.to(d)
+    logit = (xd @ shared_gate.to(d).T).to(torch.bfloat16)
+    s = torch.sigmoid(logit.to(d)).to(torch.bfloat16).to(d)
+    h = F.silu(xd @ gate_proj.to(d).T) * (xd @ up_proj.to(d).T)
+    return s * (h @ down_proj.to(d).T)
+
+
 def error_stats(out: torch.Tensor, ref: torch.Tensor) -> dict[str, float]:
     """max |out - ref| and RMS(ref) (both fp64); the bar is max_abs <= 2e-2 * rms."""
     o, r = out.double().cpu(), ref.double().cpu()

@@ -78,30 +78,43 @@ def test_gpt_oss_kernel(device):
     assert_within_tolerance(out.reshape(-1, H).cpu(), ref, "gpt-oss loader")
 
 
-def test_qwen3_kernel_includes_shared_expert(device):
+@pytest.mark.parametrize("Fs", [64, 96])  # shared intermediate = F, and 1.5 F (two blocks, the last zero-padded)
+def test_qwen3_kernel_includes_shared_expert(device, Fs):
     from torch import nn
 
+    from cernels_amd import ops
     from cernels_amd.configs.modules import DenseMlp, Qwen3NextBlock, Qwen3NextRouter
     from cernels_amd.kops.registry import qwen3_next_moe_experts as q3
 
     T, H, Fi, E, K = 160, 128, 64, 16, 4
     g = torch.Generator().manual_seed(7)
-    gate, shared, sgate = Qwen3NextRouter(H, E, K), DenseMlp(H, 64), nn.Linear(H, 1, bias=False)
+    gate, shared, sgate = Qwen3NextRouter(H, E, K), DenseMlp(H, Fs), nn.Linear(H, 1, bias=False)
     with torch.no_grad():
         for m in (gate, shared, sgate):
             for p in m.parameters():
                 p.copy_(torch.randn(p.shape, generator=g) * 0.05)
     block = Qwen3NextBlock(gate, _experts(E, H, Fi, seed=8), shared, sgate).to(device=device, dtype=torch.bfloat16)
     x = torch.randn(1, T, H, generator=g).bfloat16()
+    print(f"[qwen3 loader Fs={Fs}]", flush=True)
     out = q3.kernel(x.to(device), block).reshape(-1, H).cpu()
     xf = x.to(device).reshape(-1, H)
-    from cernels_amd import ops
     with torch.no_grad():
         _, mscores, midx = block.gate(xf)
-        shared_out = (torch.sigmoid(block.shared_expert_gate(xf)) * block.shared_expert(xf)).float().cpu()
     idx, scores = ops.moe_router(xf, block.gate.weight, None, K, ops.ROUTER_SOFTMAX_TOPK)
+    # the fused router agrees with the module's own router except where bf16 logits tie or round apart
     assert (idx.long() == midx).all(dim=1).float().mean() >= 0.95
-    e = block.experts
+    e, sh = block.experts, block.shared_expert
     routed = O.experts_fp64(x.reshape(-1, H), idx.cpu(), scores.cpu(), e.gate_up_proj.data.cpu(), e.down_proj.data.cpu())
-    # the loader adds the bf16 routed output and the bf16 shared output in bf16
-    assert_within_tolerance(out, routed + shared_out.double(), "qwen3 loader")
+    shared_ref = O.shared_expert_fp64(x.reshape(-1, H), sh.gate_proj.weight.data.cpu(), sh.up_proj.weight.data.cpu(),
+                                      sh.down_proj.weight.data.cpu(), block.shared_expert_gate.weight.data.cpu())
+    # routed and shared rows are summed in fp32 and rounded once
+    assert_within_tolerance(out, routed + shared_ref, "qwen3 loader")
+    # the same block called again reuses the packed copy; a changed shared expert is packed again
+    pk0 = block._cernels_packed_block[1][0]
+    q3.kernel(x.to(device), block)
+    assert block._cernels_packed_block[1][0] is pk0
+    with torch.no_grad():
+        sh.down_proj.weight.mul_(2.0)
+    out2 = q3.kernel(x.to(device), block).reshape(-1, H).cpu()
+    assert block._cernels_packed_block[1][0] is not pk0
+    assert_within_tolerance(out2, routed + 2.0 * shared_ref, "qwen3 loader, shared down doubled")

@@ -121,3 +121,31 @@ def test_router_rejects_bad_shapes(device):
     x2, w2, _ = _case(0, 4, 72, 8, False)
     with pytest.raises(RuntimeError):
         ops.moe_router(x2.to(device), w2.to(device), None, 2, ops.ROUTER_SOFTMAX_TOPK)  # H % 16 != 0
+
+
+@pytest.mark.parametrize("E,S,mode", [(16, 1, O.ROUTER_SOFTMAX_TOPK), (31, 1, O.ROUTER_SOFTMAX_TOPK),
+                                      (40, 2, O.ROUTER_TOPK_SOFTMAX), (63, 3, O.ROUTER_SOFTMAX_TOPK),
+                                      (512, 1, O.ROUTER_SOFTMAX_TOPK)])
+def test_router_shared_slots(device, E, S, mode):
+    """The weight's last row is the shared-expert gate: slots K..K+S-1 get ids E..E+S-1 and weight
+    bf16(sigmoid(gate logit)); the routed slots are chosen among the first E logits only."""
+    from cernels_amd import ops
+
+    T, H, K = 150, 256, 4
+    bias = mode == O.ROUTER_TOPK_SOFTMAX
+    x, w, b = _case(31 + E, T, H, E + 1, bias)
+    print(f"[router shared E={E} S={S} mode={mode}]", flush=True)
+    idx, wts, logits = ops.moe_router(x.to(device), w.to(device), None if b is None else b.to(device), K, mode,
+                                      want_logits=True, shared_slots=S)
+    idx, wts, logits = idx.cpu(), wts.cpu(), logits.cpu()
+    assert tuple(idx.shape) == (T, K + S) and tuple(logits.shape) == (T, E + 1)
+    ref_logits = O.router_logits(x, w, b)
+    dl = (logits.float() - ref_logits.float()).abs().double()
+    tol = _ulp(ref_logits).double() + H * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T)
+    assert bool((dl <= tol).all())
+    ridx, rw = O.router_select(logits[:, :E], K, mode)
+    assert torch.equal(idx[:, :K].long(), ridx)
+    assert bool(((wts[:, :K] - rw.float()).abs() <= _ulp(rw)).all())
+    assert torch.equal(idx[:, K:], (E + torch.arange(S, dtype=torch.int32)).expand(T, S))
+    sg = torch.sigmoid(logits[:, E:].float()).bfloat16()
+    assert bool(((wts[:, K:] - sg.float()).abs() <= _ulp(sg)).all())

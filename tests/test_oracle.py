@@ -340,3 +340,38 @@ def test_router_logits_identity():
     assert torch.equal(O.router_logits(x, torch.eye(24).bfloat16()), x)
     b = torch.full((24,), 0.5).bfloat16()
     assert torch.equal(O.router_logits(x, torch.eye(24).bfloat16(), b), (x.double() + 0.5).bfloat16())
+
+
+@pytest.mark.parametrize("Fs,F", [(96, 32), (64, 64), (80, 64)])
+def test_shared_expert_fp64_is_the_module_and_an_extra_expert(Fs, F):
+    """shared_expert_fp64 equals the stand-in modules' own forward (MLP in float64, gate in bf16),
+    and equals the same MLP split by ops.split_shared_expert into S experts of width F (zero-padded),
+    routed for every token with weight sigmoid(gate): the identity the fused qwen3 block relies on."""
+    from torch import nn
+
+    from cernels_amd import ops
+    from cernels_amd.configs.modules import DenseMlp
+
+    H, T = 64, 20
+    g = torch.Generator().manual_seed(Fs + F)
+    mlp, sg = DenseMlp(H, Fs), nn.Linear(H, 1, bias=False)
+    with torch.no_grad():
+        for m in (mlp, sg):
+            for p in m.parameters():
+                p.copy_((torch.randn(p.shape, generator=g) * 0.1).bfloat16().float())
+    x = torch.randn(T, H, generator=g).bfloat16()
+    gw, uw, dw, sw = (m.weight.data.bfloat16() for m in (mlp.gate_proj, mlp.up_proj, mlp.down_proj, sg))
+    ref = O.shared_expert_fp64(x, gw, uw, dw, sw)
+    with torch.no_grad():
+        s = torch.sigmoid(sg.bfloat16()(x)).double()
+        m = mlp.double()(x.double())
+    assert torch.allclose(ref, s * m, rtol=1e-12, atol=1e-14)
+    gu, dn = ops.split_shared_expert(gw, uw, dw, F)
+    S = -(-Fs // F)
+    assert tuple(gu.shape) == (S, 2 * F, H) and tuple(dn.shape) == (S, H, F)
+    idx = torch.arange(S).expand(T, S)
+    ref2 = O.experts_fp64(x, idx, s.float().expand(T, S), gu, dn)
+    assert torch.allclose(ref, ref2, rtol=1e-10, atol=1e-13)
+    # a mistake in the split (a dropped block, a transposed down) moves the result
+    ref3 = O.experts_fp64(x, idx[:, :1], s.float().expand(T, S)[:, :1], gu, dn)
+    assert S == 1 or not torch.allclose(ref, ref3, rtol=1e-6, atol=1e-8)
