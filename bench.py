@@ -17,8 +17,9 @@ For the gpt-oss and qwen3-next workloads, whose reference ops run the router ins
 fused router (``cernels_moe_router``, seeded router weights) is timed on its own as well and
 reported as ``router`` and ``op_ms_with_router``, beside the same router as torch ops (F.linear,
 softmax, topk: what the reference's loaders run) as ``router.torch_ops_ms``. ``module_ops`` times the
-reference's module-level configs ``gpt_oss_moe_experts`` and ``qwen3_next_moe_experts`` through the
-drop-in loaders (router, and for qwen3 the gated shared expert, inside the call).
+reference's module-level configs ``gpt_oss_moe_experts``, ``qwen3_next_moe_experts`` and
+``megablocks_moe`` through the drop-in loaders (router, and for qwen3 the gated shared expert, inside
+the call).
 
 Timing: W untimed warmup steps, then exactly K steps between two ``torch.cuda.synchronize()``;
 the step time is the HIP-event time of the K steps / K. Each step also records HIP events between
@@ -323,11 +324,12 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
     return rec
 
 
-MODULE_OPS = ("gpt_oss_moe_experts", "qwen3_next_moe_experts")
+MODULE_OPS = ("gpt_oss_moe_experts", "qwen3_next_moe_experts", "megablocks_moe")
 
 
 def run_module_op(name, steps, warmup, dev, log):
-    """The reference's module-level op as its config calls it (src/configs/registry/{gpt_oss,qwen3_next}_moe_experts.py):
+    """The reference's module-level op as its config calls it (src/configs/registry/{gpt_oss,qwen3_next}_moe_experts.py,
+    megablocks_moe.py):
     the drop-in loader ``kernel(x, mlp)`` / ``kernel(x, block)`` with the router (and for qwen3 the gated
     shared expert) inside the call, Python dispatch included, on seeded weights and near-uniform routing
     as the reference's configs have it. Packing happens in the first warmup call."""
@@ -341,7 +343,7 @@ def run_module_op(name, steps, warmup, dev, log):
     log(f"[{name}] module inputs built in {time.time() - t0:.1f}s")
     s = cfg.shape
     T, H, F, E, K = s.tokens, s.hidden, s.ffn, s.experts, s.top_k
-    flops = 6.0 * T * K * H * F + 2.0 * T * H * E
+    flops = (6.0 if getattr(cfg, "gated", True) else 4.0) * T * K * H * F + 2.0 * T * H * E
     shared_f = 0
     if hasattr(mod, "shared_expert"):
         shared_f = int(mod.shared_expert.gate_proj.weight.shape[0])

@@ -26,7 +26,8 @@ STATUS = {
 }
 LAYOUT_CONCAT, LAYOUT_INTERLEAVED = 0, 1
 ACT_SILU, ACT_GPTOSS = 0, 1
-GATE_UP, DOWN = 0, 1
+ACT_GELU_TANH, ACT_SILU_PLAIN, ACT_RELU = 2, 3, 4  # non-gated (megablocks)
+GATE_UP, DOWN, UP = 0, 1, 2
 ROUTER_SOFTMAX_TOPK, ROUTER_TOPK_SOFTMAX = 0, 1
 
 _P = ctypes.c_void_p
@@ -61,6 +62,8 @@ _SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P, _P],
     ),
     "cernels_moe_router": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
+    "cernels_megablocks_moe_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
+    "cernels_megablocks_moe": (ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P]),
     "cernels_moe_decode_max_tokens": (_I, []),
     "cernels_moe_decode_max_pairs": (_I, []),
     "cernels_moe_experts_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),

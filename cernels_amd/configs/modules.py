@@ -81,3 +81,51 @@ class Qwen3NextBlock(nn.Module):
         super().__init__()
         self.gate, self.experts = gate, experts
         self.shared_expert, self.shared_expert_gate = shared_expert, shared_expert_gate
+
+
+# ---- megablocks MoE (kernels-community/megablocks, a Hub package absent here): the attribute layout
+# the reference loader reads (src/kops/registry/megablocks_moe.py:10-24) and the router it calls.
+
+
+class MegablocksArgs:
+    def __init__(self, hidden, ffn, experts, top_k, activation_fn="gelu", moe_normalize_expert_weights=None):
+        self.hidden_size, self.ffn_hidden_size = hidden, ffn
+        self.moe_num_experts, self.moe_top_k = experts, top_k
+        self.activation_fn = activation_fn
+        self.moe_normalize_expert_weights = moe_normalize_expert_weights
+
+
+class MegablocksRouter(nn.Module):
+    """megablocks LearnedRouter: scores = softmax(x Wᵀ) in the input dtype, top-k, optional p-norm."""
+
+    def __init__(self, args: MegablocksArgs):
+        super().__init__()
+        self.args = args
+        self.layer = nn.Linear(args.hidden_size, args.moe_num_experts, bias=False)
+
+    def forward(self, x):
+        scores = self.layer(x.view(-1, x.shape[-1])).softmax(dim=-1)
+        w, i = torch.topk(scores, self.args.moe_top_k, dim=-1)
+        p = self.args.moe_normalize_expert_weights
+        if p:
+            w = w / torch.norm(w, p=p, dim=-1, keepdim=True)
+        return scores, w, i
+
+
+class MegablocksMlp(nn.Module):
+    def __init__(self, w1, w2):
+        super().__init__()
+        self.w1 = nn.Parameter(w1, requires_grad=False)  # [E, H, F]
+        self.w2 = nn.Parameter(w2, requires_grad=False)  # [E, F, H]
+
+
+class MegablocksExperts(nn.Module):
+    def __init__(self, args: MegablocksArgs, mlp: MegablocksMlp):
+        super().__init__()
+        self.args, self.mlp = args, mlp
+
+
+class MegablocksMoe(nn.Module):
+    def __init__(self, router: MegablocksRouter, experts: MegablocksExperts):
+        super().__init__()
+        self.router, self.experts = router, experts

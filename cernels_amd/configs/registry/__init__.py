@@ -19,7 +19,9 @@ import torch
 from torch import nn
 
 from cernels_amd.configs.base import Config
-from cernels_amd.configs.modules import DenseMlp, Experts, GptOssMlp, GptOssRouter, Qwen3NextBlock, Qwen3NextRouter
+from cernels_amd.configs.modules import (DenseMlp, Experts, GptOssMlp, GptOssRouter, MegablocksArgs, MegablocksExperts,
+                                         MegablocksMlp, MegablocksMoe, MegablocksRouter, Qwen3NextBlock,
+                                         Qwen3NextRouter)
 from cernels_amd.configs.synth import (
     ACT_GPTOSS,
     INPUT_SEED,
@@ -37,6 +39,7 @@ from cernels_amd.configs.synth import (
 from cernels_amd.kops.registry import cohere2_moe_experts as _cohere2
 from cernels_amd.kops.registry import deepseek_ocr2_moe_experts as _deepseek
 from cernels_amd.kops.registry import gpt_oss_moe_experts as _gpt_oss
+from cernels_amd.kops.registry import megablocks_moe as _megablocks
 from cernels_amd.kops.registry import qwen3_next_moe_experts as _qwen3
 
 _DS = dict(hidden=1280, ffn=896, experts=64, top_k=6)
@@ -146,6 +149,38 @@ class Qwen3NextConfig(Config):
         return x, block
 
 
+class MegablocksConfig(Config):
+    """Module-level megablocks workload (src/configs/registry/megablocks_moe.py:16-78): T=4096, H=2048,
+    F=5632, E=8, top-2, no bias, GELU (megablocks' default tanh form), router and experts in the call.
+    The reference builds the Hub module (kernels-community/megablocks), absent here; the stand-in has
+    its attribute layout and router, with seeded N(0, 0.02) weights."""
+
+    gated = False
+
+    def __init__(self):
+        self.name = "megablocks_moe"
+        self.shape = MoeShape("megablocks_moe", tokens=4096, hidden=2048, ffn=5632, experts=8, top_k=2)
+        self.op = "megablocks MoE (router + non-gated grouped experts)"
+        self.custom = staticmethod(_megablocks.kernel).__func__
+
+    def inputs(self, device, dtype=torch.bfloat16):
+        s = self.shape
+        args = MegablocksArgs(s.hidden, s.ffn, s.experts, s.top_k)
+        router = MegablocksRouter(args)
+        _seeded_normal_(router)
+        g = torch.Generator().manual_seed(WEIGHT_SEED)
+        w1 = torch.empty((s.experts, s.hidden, s.ffn), dtype=dtype)
+        w2 = torch.empty((s.experts, s.ffn, s.hidden), dtype=dtype)
+        for e in range(s.experts):
+            w1[e] = (torch.randn((s.hidden, s.ffn), generator=g) * WEIGHT_STD).to(dtype)
+        for e in range(s.experts):
+            w2[e] = (torch.randn((s.ffn, s.hidden), generator=g) * WEIGHT_STD).to(dtype)
+        moe = MegablocksMoe(router, MegablocksExperts(args, MegablocksMlp(w1, w2))).to(device=device, dtype=dtype)
+        gx = torch.Generator().manual_seed(INPUT_SEED)
+        x = torch.randn((s.tokens, s.hidden), generator=gx).to(dtype).to(device)
+        return x, moe
+
+
 def _make_configs() -> dict[str, Config]:
     cfgs: dict[str, Config] = {}
     for name, s in BASELINE_SHAPES.items():
@@ -160,6 +195,7 @@ def _make_configs() -> dict[str, Config]:
     cfgs["deepseek_ocr2_moe_experts_decode"] = ExpertsConfig(r["deepseek_ocr2_moe_experts_decode"], _deepseek.decode_kernel)
     cfgs["gpt_oss_moe_experts"] = GptOssConfig(r["gpt_oss_moe_experts"])
     cfgs["qwen3_next_moe_experts"] = Qwen3NextConfig(r["qwen3_next_moe_experts"])
+    cfgs["megablocks_moe"] = MegablocksConfig()
     return cfgs
 
 

@@ -96,7 +96,7 @@ int common_checks(const void* x, const void* w1, const void* w2, const int32_t* 
     if (!dims_ok(T, H, F, E, K)) return CERNELS_MOE_INVALID_ARGUMENT;
     if (layout != CERNELS_MOE_LAYOUT_CONCAT && layout != CERNELS_MOE_LAYOUT_INTERLEAVED)
         return CERNELS_MOE_INVALID_ARGUMENT;
-    if (act != CERNELS_MOE_ACT_SILU && act != CERNELS_MOE_ACT_GPTOSS) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (act < CERNELS_MOE_ACT_SILU || act > CERNELS_MOE_ACT_RELU) return CERNELS_MOE_INVALID_ARGUMENT;
     if (T == 0) return CERNELS_MOE_OK;
     if (!x || !w1 || !w2 || !idx || !wts || !out || !ws) return CERNELS_MOE_INVALID_ARGUMENT;
     if (!aligned16(x) || !aligned16(w1) || !aligned16(w2) || !aligned16(out) || !aligned16(ws))
@@ -107,6 +107,8 @@ int common_checks(const void* x, const void* w1, const void* w2, const int32_t* 
 }
 
 int hip_status(hipError_t e) { return e == hipSuccess ? CERNELS_MOE_OK : CERNELS_MOE_HIP_ERROR; }
+
+bool act_gated(int act) { return act == CERNELS_MOE_ACT_SILU || act == CERNELS_MOE_ACT_GPTOSS; }
 
 }  // namespace
 
@@ -182,6 +184,7 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
                                hipStream_t stream, hipEvent_t* stage_events) {
     int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
+    if (!act_gated(act)) return CERNELS_MOE_UNSUPPORTED_SHAPE;  // non-gated: packed entries only
     if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     const PrefillWs w = prefill_ws(T, H, F, E, K);
     if (workspace_bytes < w.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
@@ -206,7 +209,7 @@ int cernels_moe_experts(const void* x, const void* gate_up_proj, const float* ga
 // ---- packed weights ------------------------------------------------------------------------------
 
 size_t cernels_moe_packed_weight_bytes(int32_t H, int32_t F, int32_t E, int32_t which) {
-    if (H <= 0 || F <= 0 || E <= 0 || (which != CERNELS_MOE_GATE_UP && which != CERNELS_MOE_DOWN)) return 0;
+    if (H <= 0 || F <= 0 || E <= 0 || which < CERNELS_MOE_GATE_UP || which > CERNELS_MOE_UP) return 0;
     if (H % 64 || F % 64) return 0;
     return cmoe::packed_weight_bytes(H, F, E, which);
 }
@@ -216,7 +219,7 @@ int cernels_moe_pack_weights(const void* src, int32_t H, int32_t F, int32_t E, i
     if (!src || !dst || H <= 0 || F <= 0 || E <= 0) return CERNELS_MOE_INVALID_ARGUMENT;
     if (layout != CERNELS_MOE_LAYOUT_CONCAT && layout != CERNELS_MOE_LAYOUT_INTERLEAVED)
         return CERNELS_MOE_INVALID_ARGUMENT;
-    if (which != CERNELS_MOE_GATE_UP && which != CERNELS_MOE_DOWN) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (which < CERNELS_MOE_GATE_UP || which > CERNELS_MOE_UP) return CERNELS_MOE_INVALID_ARGUMENT;
     if (H % 64 || F % 64) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     if (!aligned16(src) || !aligned16(dst)) return CERNELS_MOE_MISALIGNED;
     return hip_status(cmoe::launch_pack(static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), E, H, F,
@@ -232,6 +235,7 @@ int cernels_moe_experts_packed_staged(const void* x, const void* gate_up_packed,
                            workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
     if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (!act_gated(act) && gate_up_bias) return CERNELS_MOE_UNSUPPORTED_SHAPE;  // non-gated: no bias
     // The packed GEMMs address x with 32-bit buffer offsets.
     if ((long long)T * H * 2 >= (1LL << 31)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     const PrefillWs w = prefill_ws(T, H, F, E, K);
@@ -256,6 +260,57 @@ int cernels_moe_experts_packed(const void* x, const void* gate_up_packed, const 
                                              workspace_bytes, stream, nullptr);
 }
 
+// ---- megablocks_moe: non-gated experts on weights as stored, packed into the workspace per call ----
+
+namespace {
+int megablocks_act(int act_id) {
+    switch (act_id) {
+        case 0: return CERNELS_MOE_ACT_GELU_TANH;
+        case 1: return CERNELS_MOE_ACT_SILU_PLAIN;
+        case 2: return CERNELS_MOE_ACT_RELU;
+        default: return -1;
+    }
+}
+struct MegaWs {
+    size_t w1, w2, run, total;
+};
+MegaWs megablocks_ws(int T, int H, int F, int E, int K) {
+    MegaWs m{};
+    m.w1 = 0;
+    m.w2 = align_up(cmoe::packed_weight_bytes(H, F, E, CERNELS_MOE_UP));
+    m.run = m.w2 + align_up(cmoe::packed_weight_bytes(H, F, E, CERNELS_MOE_DOWN));
+    m.total = m.run + prefill_ws(T, H, F, E, K).total;
+    return m;
+}
+}  // namespace
+
+size_t cernels_megablocks_moe_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t topk) {
+    if (!dims_ok(T, H, F, E, topk) || H % 64 || F % 64) return 0;
+    return megablocks_ws(T, H, F, E, topk).total;
+}
+
+int cernels_megablocks_moe(const void* x, const void* w1, const void* w2, const int32_t* indices, const float* weights,
+                           int32_t T, int32_t H, int32_t F, int32_t E, int32_t topk, int32_t act_id, void* out,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    const int act = megablocks_act(act_id);
+    if (act < 0) return CERNELS_MOE_INVALID_ARGUMENT;
+    int st = common_checks(x, w1, w2, indices, weights, T, H, F, E, topk, CERNELS_MOE_LAYOUT_INTERLEAVED, act, out,
+                           workspace);
+    if (st != CERNELS_MOE_OK || T == 0) return st;
+    if (H % 64 || F % 64 || E > kMaxExperts) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    const MegaWs m = megablocks_ws(T, H, F, E, topk);
+    if (workspace_bytes < m.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
+    char* base = static_cast<char*>(workspace);
+    // w1 [E, H, F] and w2 [E, F, H] are both k-major: the interleaved layouts of up and down
+    st = cernels_moe_pack_weights(w1, H, F, E, CERNELS_MOE_LAYOUT_INTERLEAVED, CERNELS_MOE_UP, base + m.w1, stream);
+    if (st != CERNELS_MOE_OK) return st;
+    st = cernels_moe_pack_weights(w2, H, F, E, CERNELS_MOE_LAYOUT_INTERLEAVED, CERNELS_MOE_DOWN, base + m.w2, stream);
+    if (st != CERNELS_MOE_OK) return st;
+    return cernels_moe_experts_packed(x, base + m.w1, nullptr, base + m.w2, nullptr, indices, weights, T, H, F, E,
+                                      topk, CERNELS_MOE_LAYOUT_CONCAT, act, out, base + m.run, workspace_bytes - m.run,
+                                      stream);
+}
+
 int32_t cernels_moe_decode_max_tokens(void) { return cmoe::decode_max_tokens(); }
 int32_t cernels_moe_decode_max_pairs(void) { return cmoe::decode_max_pairs(); }
 
@@ -271,7 +326,7 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
                                       size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events) {
     int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
-    if (layout != CERNELS_MOE_LAYOUT_CONCAT) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (layout != CERNELS_MOE_LAYOUT_CONCAT || !act_gated(act)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     if (T > cmoe::decode_max_tokens() || T * K > cmoe::decode_max_pairs()) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     if (H % 8 || F % 8 || !cmoe::decode_shape_supported(H, F)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     const DecodeWs w = decode_ws(T, H, F, K);

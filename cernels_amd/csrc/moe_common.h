@@ -27,6 +27,11 @@ constexpr int kLayoutInterleaved = 1;  // gate_up [E, H, 2F] (even col gate, odd
 // Activations.
 constexpr int kActSilu = 0;    // silu(gate) * up
 constexpr int kActGptOss = 1;  // (clamp(up,-7,7) + 1) * g * sigmoid(1.702 g), g = min(gate, 7)
+// Non-gated (one projection, h -> act(h)), megablocks_moe's act_id 0 / 1 / 2.
+constexpr int kActGeluTanh = 2;  // 0.5 h (1 + tanh(sqrt(2/pi) (h + 0.044715 h^3)))
+constexpr int kActSiluPlain = 3; // h sigmoid(h)
+constexpr int kActRelu = 4;      // max(h, 0)
+__host__ __device__ constexpr bool act_is_gated(int act) { return act == kActSilu || act == kActGptOss; }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -52,6 +57,22 @@ __device__ __forceinline__ float swiglu(float gate, float up) {
         up = fminf(fmaxf(up, -7.0f), 7.0f);
         const float glu = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-1.702f * gate));
         return (up + 1.0f) * glu;
+    }
+}
+
+// Non-gated activations in fp32 (src/kops/megablocks_moe/csrc/megablocks_moe.cu:78-96 lists the
+// three). GELU's tanh form is Hendrycks & Gimpel's approximation; tanh(u) = 1 - 2 / (1 + e^{2u}),
+// which saturates to +-1 through the exponential's overflow and underflow.
+template <int ACT>
+__device__ __forceinline__ float act_plain(float h) {
+    if constexpr (ACT == kActGeluTanh) {
+        const float u = 0.7978845608028654f * (h + 0.044715f * h * h * h);
+        const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(2.0f * u));
+        return 0.5f * h * (1.0f + th);
+    } else if constexpr (ACT == kActSiluPlain) {
+        return h * __builtin_amdgcn_rcpf(1.0f + __expf(-h));
+    } else {
+        return fmaxf(h, 0.0f);
     }
 }
 

@@ -41,11 +41,14 @@ constexpr int kPkBDepth = 2;                // weight stages held in registers p
 
 constexpr int kModePkGateUp = 0;
 constexpr int kModePkDown = 1;
+constexpr int kModePkUp = 2;  // non-gated first projection (megablocks): glu[r, :] = act(X[tok(r), :] · W1_e)
 
 // Packed layout of one projection, viewed as B[k][n] (reduction length Kd, KS = Kd/16 k-steps) cut
 // into NF fragments of 32 columns:
 //   gate_up: fragment c = gate columns [16c, 16c+16) then up columns [16c, 16c+16). Kd = H, NF = F/16.
 //   down:    fragment c = output columns [32c, 32c+32).                           Kd = F, NF = H/32.
+//   up:      (non-gated) fragment c = columns [32c, 32c+32), packed as a down projection with H and F
+//            exchanged.                                                           Kd = H, NF = F/32.
 // Fragments are bundled by eight (an N-tile: one fragment per wave) and stored k-step-major inside a
 // tile, so the eight waves of a workgroup read one contiguous 8 KB run per k-step. Lane l of
 // fragment (c, ks) holds B[16ks + 8(l/32) + j][column l%32 of the fragment], j = 0..7.
@@ -103,11 +106,14 @@ __global__ __launch_bounds__(256) void moe_pack_kernel(const uint16_t* __restric
 }
 
 size_t packed_weight_bytes(int H, int F, int E, int which) {
-    (void)which;  // both projections keep their element count: 2FH (gate_up) and HF (down)
+    // every projection keeps its element count: 2FH (gate_up), HF (down, up)
     return which == 0 ? (size_t)E * 2 * F * H * 2 : (size_t)E * H * F * 2;
 }
 
 hipError_t launch_pack(const uint16_t* src, uint16_t* dst, int E, int H, int F, int layout, int which, hipStream_t s) {
+    // up ([E, F, H] concat = rows are outputs, or [E, H, F] interleaved = k-major) is a down
+    // projection with H and F exchanged
+    if (which == 2) return launch_pack(src, dst, E, F, H, layout, 1, s);
     const long long chunks = (long long)E * (which == 0 ? 2LL * F * H : (long long)H * F) / 8;  // = E*NF*KS*64
     const unsigned grid = (unsigned)((chunks + 255) / 256);
     if (which == 0) {
@@ -154,6 +160,9 @@ using IC = std::integral_constant<int, N>;
 template <int MODE, int ACT, bool HAS_BIAS, bool XPF, bool ODD>
 __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams prm) {
     static_assert(XPF || ODD, "a single-stage reduction is odd");
+    static_assert(MODE != kModePkUp || !HAS_BIAS, "the non-gated projection has no bias");
+    // the first projection gathers token rows of x through the pair list; down reads its own glu rows
+    constexpr bool kGather = MODE != kModePkDown;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kPkABytes];
     // Epilogue tables, double-buffered by item parity: row -> pair and routing weight (GEMM2), and
     // the N-tile's bias (GEMM1: 128 gate then 128 up entries; GEMM2: 256 columns).
@@ -190,11 +199,11 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     //   B: the wave's fragment run from k-step 0; lane offset lane*16, k-step offsets uniform.
     auto a_row = [&](const WorkItem& w, int i) { return w.row_begin + min((tid >> 3) + 64 * i, w.rows - 1); };
     auto a_off = [&](const WorkItem& w, int src_row) {
-        const int r = MODE == kModePkGateUp ? src_row : src_row - w.row_begin;
+        const int r = kGather ? src_row : src_row - w.row_begin;
         return (uint32_t)r * (uint32_t)(Kd * 2) + (uint32_t)a_chunk * 16u;
     };
     auto a_rsrc = [&](const WorkItem& w) {
-        if constexpr (MODE == kModePkGateUp)
+        if constexpr (kGather)
             return __builtin_amdgcn_make_buffer_rsrc((void*)prm.A, (short)0, prm.a_bytes, kBufferWord3);
         else
             return __builtin_amdgcn_make_buffer_rsrc((void*)(prm.A + (long long)w.row_begin * Kd), (short)0,
@@ -260,7 +269,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         int pr[kPkMB / 2];
 #pragma unroll
         for (int i = 0; i < kPkMB / 2; ++i) {
-            if constexpr (MODE == kModePkGateUp) pr[i] = prm.sorted_pairs[a_row(w, i)];
+            if constexpr (kGather) pr[i] = prm.sorted_pairs[a_row(w, i)];
             else pr[i] = a_row(w, i);
         }
         int pair = 0;
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         if constexpr (HAS_BIAS) bias = tab_bias(w);
 #pragma unroll
         for (int i = 0; i < kPkMB / 2; ++i)
-            a_cur[i] = a_off(w, MODE == kModePkGateUp ? pr[i] / prm.topk : pr[i]);
+            a_cur[i] = a_off(w, kGather ? pr[i] / prm.topk : pr[i]);
         if constexpr (MODE == kModePkDown) rw = prm.route_w[pair];
 #pragma unroll
         for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_cur, a_cur[i], 0);
@@ -331,7 +340,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     if constexpr (XPF) {
 #pragma unroll
                         for (int i = 0; i < kPkMB / 2; ++i)
-                            a_cur[i] = a_off(nx, MODE == kModePkGateUp ? nxr[i] / prm.topk : nxr[i]);
+                            a_cur[i] = a_off(nx, kGather ? nxr[i] / prm.topk : nxr[i]);
 #pragma unroll
                         for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_nx, a_cur[i], 0);
                         if constexpr (MODE == kModePkDown) nw = prm.route_w[npair];
@@ -342,7 +351,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     if constexpr (KIND == 1) {
 #pragma unroll
                         for (int i = 0; i < kPkMB / 2; ++i) {
-                            if constexpr (MODE == kModePkGateUp) nxr[i] = prm.sorted_pairs[a_row(nx, i)];
+                            if constexpr (kGather) nxr[i] = prm.sorted_pairs[a_row(nx, i)];
                             else nxr[i] = a_row(nx, i);
                         }
                         if constexpr (MODE == kModePkDown) npair = tab_pair(nx);
@@ -468,6 +477,24 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                                 v[jj] = swiglu<ACT>(gv, uv);
                             }
                             *reinterpret_cast<u32x2*>(glu + (long long)(row_begin + row) * prm.F + 16 * fc + 8 * i + c4) =
+                                u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                        }
+                    }
+                }
+            } else if constexpr (MODE == kModePkUp) {
+                // 16 columns of the fragment per lane (8i + c4 + jj), activation, bf16 glu row.
+                uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+#pragma unroll
+                for (int mb = 0; mb < kPkMB; ++mb) {
+                    if (mb >= nmb) break;
+                    const int row = mb * 32 + (lane & 31);
+                    if (row < rows) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float v[4];
+#pragma unroll
+                            for (int jj = 0; jj < 4; ++jj) v[jj] = act_plain<ACT>(acc[mb][4 * i + jj]);
+                            *reinterpret_cast<u32x2*>(glu + (long long)(row_begin + row) * prm.F + 32 * fc + 8 * i + c4) =
                                 u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                         }
                     }
@@ -598,7 +625,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.route_w = route_w;
     g1.out = glu;
     g1.Kd = H;
-    g1.NF = F / 16;
+    g1.NF = act_is_gated(act) ? F / 16 : F / 32;
     g1.KS = H / 16;
     g1.fw = pick_fw((long long)T * K, E, g1.NF, H, pk_cu_count());
     g1.n_tiles = ceil_div(g1.NF, g1.fw);
@@ -610,9 +637,15 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     if (act == kActSilu)
         st = b1 ? launch_pk_t<kModePkGateUp, kActSilu, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActSilu, false>(g1, max_tiles, s);
-    else
+    else if (act == kActGptOss)
         st = b1 ? launch_pk_t<kModePkGateUp, kActGptOss, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActGptOss, false>(g1, max_tiles, s);
+    else if (act == kActGeluTanh)  // non-gated: no first-projection bias (checked by the caller)
+        st = launch_pk_t<kModePkUp, kActGeluTanh, false>(g1, max_tiles, s);
+    else if (act == kActSiluPlain)
+        st = launch_pk_t<kModePkUp, kActSiluPlain, false>(g1, max_tiles, s);
+    else
+        st = launch_pk_t<kModePkUp, kActRelu, false>(g1, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(2);
     PkParams g2 = g1;

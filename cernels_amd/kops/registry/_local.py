@@ -13,6 +13,7 @@ _OPS = {
     "deepseek_ocr2_moe_experts": ("deepseek_ocr2_moe_experts", "deepseek_ocr2_moe_experts_decode"),
     "qwen3_next_moe_experts": ("qwen3_next_moe_experts",),
     "gpt_oss_moe_experts": ("gpt_oss_moe_experts",),
+    "megablocks_moe": ("megablocks_moe",),
 }
 
 

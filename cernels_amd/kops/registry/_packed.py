@@ -71,3 +71,16 @@ def packed_block(block):
     val = (pk, rw, S)
     setattr(block, _BLOCK_ATTR, (key, val))
     return val
+
+
+def packed_megablocks(mlp, act):
+    """megablocks MLP (``w1`` [E, H, F], ``w2`` [E, F, H]) packed for a non-gated activation, cached on
+    the MLP module with the same keying as ``packed_experts``."""
+    key = _key((mlp.w1, mlp.w2)) + (act,)
+    cached = getattr(mlp, _ATTR, None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    with torch.no_grad():
+        pk = ops.pack_experts_nongated(mlp.w1.data, mlp.w2.data, act)
+    setattr(mlp, _ATTR, (key, pk))
+    return pk

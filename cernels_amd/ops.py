@@ -17,8 +17,12 @@ import ctypes
 import torch
 
 from cernels_amd import _native
-from cernels_amd._native import (ACT_GPTOSS, ACT_SILU, LAYOUT_CONCAT, LAYOUT_INTERLEAVED, ROUTER_SOFTMAX_TOPK,
-                                 ROUTER_TOPK_SOFTMAX, check)
+from cernels_amd._native import (ACT_GELU_TANH, ACT_GPTOSS, ACT_RELU, ACT_SILU, ACT_SILU_PLAIN, LAYOUT_CONCAT,
+                                 LAYOUT_INTERLEAVED, ROUTER_SOFTMAX_TOPK, ROUTER_TOPK_SOFTMAX, check)
+
+# megablocks_moe's act_id (src/kops/registry/megablocks_moe.py:7 names them; csrc/megablocks_moe.cu:78-96)
+# -> the library's non-gated activation
+MEGABLOCKS_ACTS = {0: ACT_GELU_TANH, 1: ACT_SILU_PLAIN, 2: ACT_RELU}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -318,10 +322,54 @@ def gpt_oss_moe_experts(x, gate_up_proj, gate_up_bias, down_proj, down_bias, ind
                        gate_up_bias=gate_up_bias, down_bias=down_bias)
 
 
+def pack_experts_nongated(w1: torch.Tensor, w2: torch.Tensor, act: int) -> PackedExperts:
+    """Pack megablocks-layout experts (w1 [E, H, F], w2 [E, F, H]) for moe_experts_packed with a
+    non-gated activation (ACT_GELU_TANH, ACT_SILU_PLAIN or ACT_RELU)."""
+    _require(act in MEGABLOCKS_ACTS.values(), "act must be a non-gated activation")
+    _require(w1.dim() == 3 and w2.dim() == 3, "w1 [E, H, F] and w2 [E, F, H]")
+    E, H, F = map(int, w1.shape)
+    _require(tuple(w2.shape) == (E, F, H), "w2 must be [E, F, H]")
+    up = pack_weights(w1.contiguous(), LAYOUT_INTERLEAVED, _native.UP, H, F)
+    dn = pack_weights(w2.contiguous(), LAYOUT_INTERLEAVED, _native.DOWN, H, F)
+    return PackedExperts(up, dn, H, F, E, act, LAYOUT_CONCAT)
+
+
+def megablocks_moe(x, w1, w2, indices, weights, topk, act_id):
+    """megablocks_moe(x [T,H], w1 [E,H,F], w2 [E,F,H], indices [T,topk] int32, weights [T,topk] fp32,
+    topk, act_id) -> [T,H] bf16 (src/kops/megablocks_moe/torch-ext/torch_binding.cpp,
+    csrc/megablocks_moe.cu:141-254): sum_k weights * act(x w1[e]) w2[e], act_id 0 = GELU (tanh form),
+    1 = SiLU, 2 = ReLU. The weights are packed into the workspace on every call, as the op takes them
+    as stored; the megablocks loader packs once per module instead."""
+    _require(int(act_id) in MEGABLOCKS_ACTS, "act_id must be 0 (gelu), 1 (silu) or 2 (relu)")
+    for t, name in ((x, "x"), (w1, "w1"), (w2, "w2"), (indices, "indices"), (weights, "weights")):
+        _require(t.is_cuda and t.is_contiguous(), f"{name} must be a contiguous CUDA tensor")
+    _require(x.dtype == torch.bfloat16 and w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16,
+             "x, w1, w2 must be bf16")
+    _require(indices.dtype == torch.int32 and weights.dtype == torch.float32, "indices int32, weights fp32")
+    T, H = map(int, x.shape)
+    E, H1, F = map(int, w1.shape)
+    K = int(topk)
+    _require(H1 == H and tuple(w2.shape) == (E, F, H), "w1 must be [E, H, F] and w2 [E, F, H]")
+    _require(tuple(indices.shape) == (T, K) and tuple(weights.shape) == (T, K), "indices / weights must be [T, topk]")
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
+    if T == 0:
+        return out
+    L = _native.lib()
+    with torch.cuda.device(x.device):
+        nbytes = L.cernels_megablocks_moe_workspace_bytes(T, H, F, E, K)
+        _require(nbytes > 0, f"unsupported shape H={H} F={F} (need H % 64 == 0, F % 64 == 0)")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        st = L.cernels_megablocks_moe(_ptr(x), _ptr(w1), _ptr(w2), _ptr(indices), _ptr(weights), T, H, F, E, K,
+                                      int(act_id), _ptr(out), _ptr(ws), ctypes.c_size_t(nbytes), _stream(x.device))
+    check(st, "megablocks_moe")
+    return out
+
+
 __all__ = [
     "moe_experts", "route", "decode_supported", "PackedExperts", "pack_weights", "pack_experts", "moe_experts_packed",
     "cohere2_moe_experts", "cohere2_moe_experts_decode",
     "deepseek_ocr2_moe_experts", "deepseek_ocr2_moe_experts_decode",
-    "qwen3_next_moe_experts", "gpt_oss_moe_experts",
-    "LAYOUT_CONCAT", "LAYOUT_INTERLEAVED", "ACT_SILU", "ACT_GPTOSS",
+    "qwen3_next_moe_experts", "gpt_oss_moe_experts", "megablocks_moe", "pack_experts_nongated", "moe_router",
+    "split_shared_expert", "pack_experts_with_shared",
+    "LAYOUT_CONCAT", "LAYOUT_INTERLEAVED", "ACT_SILU", "ACT_GPTOSS", "ACT_GELU_TANH", "ACT_SILU_PLAIN", "ACT_RELU",
 ]

@@ -47,11 +47,16 @@ enum cernels_moe_status {
 
 enum cernels_moe_layout { CERNELS_MOE_LAYOUT_CONCAT = 0, CERNELS_MOE_LAYOUT_INTERLEAVED = 1 };
 enum cernels_moe_act {
-    CERNELS_MOE_ACT_SILU = 0,   /* silu(gate) * up */
-    CERNELS_MOE_ACT_GPTOSS = 1  /* (clamp(up,-7,7) + 1) * g * sigmoid(1.702 g), g = min(gate, 7) */
+    CERNELS_MOE_ACT_SILU = 0,       /* silu(gate) * up */
+    CERNELS_MOE_ACT_GPTOSS = 1,     /* (clamp(up,-7,7) + 1) * g * sigmoid(1.702 g), g = min(gate, 7) */
+    /* non-gated (one first projection H -> F, megablocks_moe; packed entries only, no first-projection bias): */
+    CERNELS_MOE_ACT_GELU_TANH = 2,  /* 0.5 h (1 + tanh(sqrt(2/pi) (h + 0.044715 h^3))) */
+    CERNELS_MOE_ACT_SILU_PLAIN = 3, /* h sigmoid(h) */
+    CERNELS_MOE_ACT_RELU = 4        /* max(h, 0) */
 };
 
-enum cernels_moe_projection { CERNELS_MOE_GATE_UP = 0, CERNELS_MOE_DOWN = 1 };
+/* GATE_UP: gated first projection; DOWN: second projection; UP: non-gated first projection. */
+enum cernels_moe_projection { CERNELS_MOE_GATE_UP = 0, CERNELS_MOE_DOWN = 1, CERNELS_MOE_UP = 2 };
 
 const char* cernels_moe_version(void);
 const char* cernels_moe_status_string(int status);
@@ -103,8 +108,11 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
  * expert) and accepts either source layout; the packed format no longer depends on the source
  * layout. No counterpart op in the reference: these entries are the fast path behind the same
  * loaders.
- *   which: CERNELS_MOE_GATE_UP (src [E,2F,H] concat or [E,H,2F] interleaved) or CERNELS_MOE_DOWN
- *          (src [E,H,F] concat or [E,F,H] interleaved).
+ *   which: CERNELS_MOE_GATE_UP (src [E,2F,H] concat or [E,H,2F] interleaved), CERNELS_MOE_DOWN
+ *          (src [E,H,F] concat or [E,F,H] interleaved) or CERNELS_MOE_UP (non-gated first projection,
+ *          src [E,F,H] concat or [E,H,F] interleaved, i.e. megablocks' w1).
+ *   act: a non-gated act (GELU_TANH, SILU_PLAIN, RELU) takes gate_up_packed packed as CERNELS_MOE_UP
+ *          and no gate_up_bias.
  *   bias_layout (experts_packed): column order of gate_up_bias, CERNELS_MOE_LAYOUT_CONCAT
  *          ([gate F | up F]) or CERNELS_MOE_LAYOUT_INTERLEAVED (gate/up alternating).
  * Limits: H % 64 == 0, F % 64 == 0, E <= 1024, K <= 4096; experts_packed also T*H*2 < 2^31 (32-bit offsets).
@@ -167,6 +175,19 @@ enum cernels_moe_router_mode { CERNELS_MOE_ROUTER_SOFTMAX_TOPK = 0, CERNELS_MOE_
 int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,
                        int32_t E, int32_t K, int32_t mode, int32_t renorm, int32_t shared_slots, int32_t* indices,
                        float* weights, void* logits, hipStream_t stream);
+
+/* ---- megablocks_moe (src/kops/megablocks_moe/torch-ext/torch_binding.cpp; csrc/megablocks_moe.cu:141-254) --
+ * Non-gated experts: out = sum_k w_k * act(x W1[e_k]) W2[e_k], x [T,H], w1 [E,H,F], w2 [E,F,H] bf16,
+ * indices [T,topk] int32, weights [T,topk] fp32, act_id 0 = GELU (tanh form), 1 = SiLU, 2 = ReLU, as
+ * the reference op's. The weights are packed into the workspace on every call (the reference op
+ * also takes the weights as stored); a caller that keeps them resident packs once with
+ * cernels_moe_pack_weights (CERNELS_MOE_UP / CERNELS_MOE_DOWN, interleaved layout) and calls
+ * cernels_moe_experts_packed, as the megablocks loader here does.
+ * Limits: H % 64 == 0, F % 64 == 0, E <= 1024, topk <= 4096, T*H*2 < 2^31. */
+size_t cernels_megablocks_moe_workspace_bytes(int32_t T, int32_t H, int32_t F, int32_t E, int32_t topk);
+int cernels_megablocks_moe(const void* x, const void* w1, const void* w2, const int32_t* indices, const float* weights,
+                           int32_t T, int32_t H, int32_t F, int32_t E, int32_t topk, int32_t act_id, void* out,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- the reference's per-model ops, same argument order as their torch schemas ----------------
  * cohere2_moe_experts(Tensor x, Tensor gate_up_proj, Tensor down_proj, Tensor indices,

@@ -206,6 +206,30 @@ def router_select(logits, top_k: int, mode: int, renorm: bool = True):
     return idx, w.to(torch.bfloat16)
 
 
+MEGABLOCKS_ACT_FNS = {0: lambda h: F.gelu(h, approximate="tanh"), 1: F.silu, 2: F.relu}
+
+
+def megablocks_fp64(x, top_k_index, top_k_weights, w1, w2, act_id: int):
+    """megablocks_moe (src/kops/megablocks_moe/csrc/megablocks_moe.cu:141-254): for every (token, slot)
+    with expert id e in [0, E) (.cu:32,56), ``weight * act(x w1[e]) w2[e]`` summed per token; w1 is
+    [E, H, F], w2 [E, F, H]; act_id 0 = GELU tanh form (.cu:81-84), 1 = SiLU, 2 = ReLU (.cu:86-96).
+    Float64 with no intermediate rounding (the reference rounds both GEMM outputs to bf16). Returns
+    fp64 [T, H]."""
+    d = torch.float64
+    act = MEGABLOCKS_ACT_FNS[int(act_id)]
+    x, w = x.to(d), top_k_weights.to(d)
+    E = w1.shape[0]
+    out = torch.zeros(x.shape, dtype=d)
+    idx = _valid_mask_index(top_k_index, E)
+    for e in torch.unique(idx).tolist():
+        if e == E:
+            continue
+        tpos, kpos = torch.where(idx == e)
+        y = act(x[tpos] @ w1[e].to(d)) @ w2[e].to(d)
+        out.index_add_(0, tpos, y * w[tpos, kpos, None])
+    return out
+
+
 def shared_expert_fp64(x, gate_proj, up_proj, down_proj, shared_gate):
     """``sigmoid(shared_expert_gate(x)) * shared_expert(x)`` of Qwen3NextSparseMoeBlock
     (transformers/models/qwen3_next/modeling_qwen3_next.py:789-795, Qwen3NextMLP :730-745 style

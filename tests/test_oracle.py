@@ -375,3 +375,49 @@ def test_shared_expert_fp64_is_the_module_and_an_extra_expert(Fs, F):
     # a mistake in the split (a dropped block, a transposed down) moves the result
     ref3 = O.experts_fp64(x, idx[:, :1], s.float().expand(T, S)[:, :1], gu, dn)
     assert S == 1 or not torch.allclose(ref, ref3, rtol=1e-6, atol=1e-8)
+
+
+def _megablocks_case(T=12, H=16, F=24, E=5, K=2, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).bfloat16()
+    w1 = (torch.randn(E, H, F, generator=g) * 0.2).bfloat16()
+    w2 = (torch.randn(E, F, H, generator=g) * 0.2).bfloat16()
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).int()
+    wt = torch.rand(T, K, generator=g)
+    return x, w1, w2, idx, wt
+
+
+def test_megablocks_fp64_brute_force_and_closed_forms():
+    """Per-(token, slot) brute force with the activations written out (GELU's tanh form from its
+    formula, not torch's), ids outside [0, E) skipped, linearity in the routing weights."""
+    import math
+
+    x, w1, w2, idx, wt = _megablocks_case()
+    idx[0, 1] = -1
+    idx[3, 0] = 5  # == E: skipped
+    acts = {0: lambda h: 0.5 * h * (1 + torch.tanh(math.sqrt(2 / math.pi) * (h + 0.044715 * h ** 3))),
+            1: lambda h: h / (1 + torch.exp(-h)), 2: lambda h: torch.clamp(h, min=0)}
+    for a, fn in acts.items():
+        ref = O.megablocks_fp64(x, idx, wt, w1, w2, a)
+        bf = torch.zeros(ref.shape, dtype=torch.float64)
+        for t in range(x.shape[0]):
+            for k in range(idx.shape[1]):
+                e = int(idx[t, k])
+                if 0 <= e < w1.shape[0]:
+                    h = x[t].double() @ w1[e].double()
+                    bf[t] += float(wt[t, k]) * (fn(h) @ w2[e].double())
+        assert torch.allclose(ref, bf, rtol=1e-12, atol=1e-12), a
+        assert torch.allclose(O.megablocks_fp64(x, idx, 2 * wt, w1, w2, a), 2 * ref, rtol=1e-12, atol=1e-12)
+
+
+def test_megablocks_silu_is_a_gated_expert_with_unit_up():
+    """silu(x w1) w2 equals the gated experts' silu(gate) * up with gate = w1ᵀ, up weights 0 and up
+    bias 1: ties megablocks_fp64 to experts_fp64, which the golden fixtures pin."""
+    x, w1, w2, idx, wt = _megablocks_case(seed=3)
+    E, H, F = w1.shape
+    gate_up = torch.cat([w1.transpose(1, 2), torch.zeros(E, F, H, dtype=w1.dtype)], dim=1)  # [E, 2F, H]
+    bias = torch.cat([torch.zeros(E, F), torch.ones(E, F)], dim=1)
+    ref = O.experts_fp64(x, idx, wt, gate_up, w2.transpose(1, 2), gate_up_bias=bias)
+    assert torch.allclose(O.megablocks_fp64(x, idx, wt, w1, w2, 1), ref, rtol=1e-12, atol=1e-12)
+    # the other activations differ from silu on the same inputs (a swapped act id would show)
+    assert not torch.allclose(O.megablocks_fp64(x, idx, wt, w1, w2, 0), ref, rtol=1e-6, atol=1e-8)
