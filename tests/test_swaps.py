@@ -82,3 +82,65 @@ def test_swapped_module_matches_oracle(device):
         out = ex(c["x"][rows].to(device), c["idx"][rows].to(device), c["w"][rows].to(device))
         ref = O.experts_fp64(c["x"][rows], c["idx"][rows], c["w"][rows], c["W1"], c["W2"])
         assert_within_tolerance(out.cpu(), ref, f"swapped rows {rows}")
+
+
+# ---- whole-model runner (cernels_amd.modeling.main) on the real transformers architectures ----
+
+_TINY_NMC = dict(hidden_size=128, num_attention_heads=4, num_key_value_heads=2, head_dim=32, intermediate_size=64,
+                 prefix_dense_intermediate_size=256, num_experts=8, vocab_size=1000)
+_TINY_DS = dict(hidden_size=128, intermediate_size=256, moe_intermediate_size=64, num_attention_heads=4,
+                num_key_value_heads=4, n_routed_experts=8, num_experts_per_tok=2, vocab_size=1000)
+
+
+def test_model_configs_match_the_documented_architectures():
+    from cernels_amd.modeling import models as M
+
+    c = M.make_config(M.NORTH_MINI_CODE)
+    assert (c.num_hidden_layers, c.hidden_size, c.intermediate_size, c.num_experts, c.num_experts_per_tok) == \
+        (49, 2048, 768, 128, 8)
+    assert c.mlp_layer_types[0] == "dense" and set(c.mlp_layer_types[1:]) == {"sparse"}
+    assert (c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.sliding_window) == (32, 4, 128, 4096)
+    assert c.expert_selection_fn == "sigmoid" and c.norm_topk_prob is False and c.num_shared_experts == 0
+    d = M.make_config(M.DEEPSEEK_OCR_2).text_config
+    assert (d.num_hidden_layers, d.hidden_size, d.moe_intermediate_size, d.n_routed_experts, d.num_experts_per_tok,
+            d.n_shared_experts) == (12, 1280, 896, 64, 6, 2)
+    assert d.mlp_layer_types[0] == "dense" and set(d.mlp_layer_types[1:]) == {"sparse"}
+
+
+@pytest.mark.parametrize("name,tiny,cls", [("north_mini_code", _TINY_NMC, "Cohere2MoeExperts"),
+                                           ("deepseek_ocr_2", _TINY_DS, "DeepseekOcr2TextExperts")])
+def test_swap_targets_every_moe_layer_of_the_real_model(name, tiny, cls):
+    from cernels_amd.modeling import models as M
+
+    model = M.build(M.SPECS[name], device="cpu", layers=3, **tiny)
+    n = sum(type(m).__name__ == cls for m in model.modules())
+    assert n == 2  # layer 0 is dense
+    fn, variants = swaps.SWAPS[name]
+    assert fn(model, variants[-1]) == n
+    assert all("forward" in vars(m) for m in model.modules() if type(m).__name__ == cls)
+    fn(model, "stock")
+    assert not any("forward" in vars(m) for m in model.modules() if type(m).__name__ == cls)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,tiny", [("north_mini_code", _TINY_NMC), ("deepseek_ocr_2", _TINY_DS)])
+def test_whole_model_runner_on_a_small_model(device, name, tiny):
+    """Every variant runs end to end through generate(); the swapped model's last prefill logits stay
+    close to stock (bf16 model, fp32-accumulating experts)."""
+    from cernels_amd.modeling import main as runner
+    from cernels_amd.modeling import models as M
+
+    spec = M.SPECS[name]
+    model = M.build(spec, device="cuda", layers=3, **tiny)
+    inputs = M.prompt_ids(spec, 40, "cuda", vocab=1000)
+    print(f"[whole model {name}]", flush=True)
+    res = runner.run(model, inputs, name, gate_tokens=6, decode_tokens=6, runs=1, min_run_time=0.05)
+    _, variants = swaps.SWAPS[name]
+    assert list(res) == list(variants)
+    stock = runner.last_logits(model, inputs)
+    for v in variants[1:]:
+        swaps.SWAPS[name][0](model, v)
+        lv = runner.last_logits(model, inputs)
+        assert float((lv - stock).abs().max()) <= 0.05 * float(stock.abs().max()) + 1e-3, v
+        assert res[v]["decode_tok_s"] > 0
+    swaps.SWAPS[name][0](model, "stock")
