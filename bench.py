@@ -132,7 +132,12 @@ def roofline_of(flops, nbytes, ms):
 
 
 def _timed_steps(step, stages, steps, warmup, hip, stream):
-    """Runs warmup + timed steps; returns (ms per step, wall ms per step, {stage: mean ms})."""
+    """Runs warmup + timed steps; returns (ms per step, wall ms per step, {stage: mean ms}).
+
+    The step time comes from K steps with no events between their kernels (only the two events
+    around the K steps). A second pass of K steps records an event between every two kernels for
+    the per-stage breakdown; those events add a little time of their own, so the stage times sum to
+    slightly more than the step time."""
     import torch
 
     for i in range(warmup):
@@ -140,19 +145,24 @@ def _timed_steps(step, stages, steps, warmup, hip, stream):
     torch.cuda.synchronize()
     nst = len(stages) + 1
     ev = Events(hip, nst * steps + 2)
-    arrs_keep = [(ctypes.c_void_p * nst)(*ev.ev[2 + s * nst: 2 + (s + 1) * nst]) for s in range(steps)]
-    arrs = [ctypes.cast(a, ctypes.c_void_p) for a in arrs_keep]
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     hip.hipEventRecord(ev.ev[0], ctypes.c_void_p(stream))
     for s in range(steps):
-        step(s, arrs[s])
+        step(s, None)
     hip.hipEventRecord(ev.ev[1], ctypes.c_void_p(stream))
     torch.cuda.synchronize()
     wall = (time.perf_counter() - wall0) * 1e3 / steps
     ms = ev.ms(0, 1) / steps
-    stage_ms = {name: statistics.mean(ev.ms(2 + s * nst + j, 2 + s * nst + j + 1) for s in range(steps))
-                for j, name in enumerate(stages)}
+    stage_ms = {}
+    if stages:
+        arrs_keep = [(ctypes.c_void_p * nst)(*ev.ev[2 + s * nst: 2 + (s + 1) * nst]) for s in range(steps)]
+        arrs = [ctypes.cast(a, ctypes.c_void_p) for a in arrs_keep]
+        for s in range(steps):
+            step(s, arrs[s])
+        torch.cuda.synchronize()
+        stage_ms = {name: statistics.mean(ev.ms(2 + s * nst + j, 2 + s * nst + j + 1) for s in range(steps))
+                    for j, name in enumerate(stages)}
     ev.close()
     return ms, wall, stage_ms
 
