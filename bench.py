@@ -22,8 +22,9 @@ reference's module-level configs ``gpt_oss_moe_experts``, ``qwen3_next_moe_exper
 the call).
 
 Timing: W untimed warmup steps, then exactly K steps between two ``torch.cuda.synchronize()``;
-the step time is the HIP-event time of the K steps / K. Each step also records HIP events between
-its kernels on the launch stream, which gives each kernel's average duration (``stages``).
+the step time is the HIP-event time of the K steps / K, with no events between a step's kernels. A
+second pass of K steps records HIP events between the kernels on the launch stream, which gives
+each kernel's average duration (``stages``).
 Cold cache: steps rotate over R copies of the expert weights so that the bytes touched per
 rotation exceed 1 GiB (4x the 256 MB Infinity Cache).
 
