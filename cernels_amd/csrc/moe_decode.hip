@@ -22,7 +22,6 @@ constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kDecMaxPairs = 256;
 constexpr int kDecMaxTokens = 64;
 constexpr int kDecMaxExperts = 1024;  // bitmap of 32 words
-constexpr int kDecDownRows = 2;       // output rows per down workgroup
 constexpr int kDnWaves = 8;           // waves per down workgroup
 constexpr int kDnThreads = kDnWaves * kWave;
 
@@ -180,17 +179,17 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
 }
 
 // out[t, h] = bf16( sum over valid slots k of w_{t,k} * (glu[t*K+k] . W2_{e}[h] + b2_e[h]) ).
-// grid: ceil(H / 2), 8 waves. Wave w takes the pairs p = w, w+8, ..., Q at a time (all Q pairs'
+// grid: ceil(H / HB), 8 waves; HB = 4 output rows per workgroup while that still leaves two
+// workgroups per CU and rows are short (F <= 1024), else 2. Wave w takes the pairs p = w, w+8, ..., Q at a time (all Q pairs'
 // weight rows and glu rows in flight together), accumulating per (token, row) in the lane that
 // holds the token; the eight waves' partial sums are added in wave order at the end, so the result
 // does not depend on timing. Pair indices are wave-uniform, so expert ids and routing weights come
 // through the scalar cache.
-template <bool HAS_BIAS, int MAXC, int Q>
+template <bool HAS_BIAS, int MAXC, int Q, int HB>
 __global__ __launch_bounds__(kDnThreads) void moe_decode_down_kernel(
     const uint16_t* __restrict__ glu, const uint16_t* __restrict__ w2, const float* __restrict__ b2,
     const int32_t* __restrict__ idx, const float* __restrict__ route_w, uint16_t* __restrict__ out, int T, int H,
     int F, int E, int K) {
-    constexpr int HB = kDecDownRows;
     __shared__ float part[kDnWaves][HB][kDecMaxTokens];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -277,14 +276,36 @@ static void launch_gateup_t(const uint16_t* x, const uint16_t* w1, const float* 
         launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, T, H, F, E, K, s);
 }
 
-// Q (pairs in flight per wave) shrinks as rows widen, to bound the registers they take.
+static int g_dec_cu_count = 0;
+
+static int dec_cu_count() {
+    if (g_dec_cu_count == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_dec_cu_count = n;
+        else
+            g_dec_cu_count = 256;
+    }
+    return g_dec_cu_count;
+}
+
+// Q (pairs in flight per wave) shrinks as rows widen, to bound the registers they take. Four
+// output rows per workgroup (with two pairs in flight) when H / 4 still fills every CU twice:
+// fewer, larger workgroups stream the same rows with less per-workgroup overhead.
 template <bool HAS_BIAS, int MAXC>
 static void launch_down_t(const uint16_t* glu, const uint16_t* w2, const float* b2, const int32_t* idx,
                           const float* route_w, uint16_t* out, int T, int H, int F, int E, int K, hipStream_t s) {
+    if constexpr (MAXC <= 2) {
+        if (H / 4 >= 2 * dec_cu_count()) {
+            hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, 2, 4>), dim3(ceil_div(H, 4)), dim3(kDnThreads), 0,
+                               s, glu, w2, b2, idx, route_w, out, T, H, F, E, K);
+            return;
+        }
+    }
     constexpr int Q = MAXC <= 2 ? 4 : (MAXC <= 4 ? 2 : 1);
-    dim3 grid(ceil_div(H, kDecDownRows));
-    hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, Q>), grid, dim3(kDnThreads), 0, s, glu, w2, b2, idx,
-                       route_w, out, T, H, F, E, K);
+    hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, Q, 2>), dim3(ceil_div(H, 2)), dim3(kDnThreads), 0, s,
+                       glu, w2, b2, idx, route_w, out, T, H, F, E, K);
 }
 
 // MAXC = 16-byte chunks per lane per row = ceil(len / 512); supported up to 8 (len <= 4096).
