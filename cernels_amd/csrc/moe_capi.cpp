@@ -12,7 +12,7 @@ namespace cmoe {
 struct GemmParams;
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        hipStream_t stream);
+                        int32_t* sched, hipStream_t stream);
 size_t route_workspace_bytes(int T, int K, int E);
 int gemm_tile_m();
 int packed_tile_m();
@@ -61,7 +61,7 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     size_t o = 0;
     w.offsets = o;      o = align_up(o + sizeof(int32_t) * (E + 1));
     w.tile_offsets = o; o = align_up(o + sizeof(int32_t) * (E + 1));
-    w.meta = o;         o = align_up(o + sizeof(int32_t) * 4);
+    w.meta = o;         o = align_up(o + sizeof(int32_t) * 32);  // [0..1] route totals, [8..23] GEMM work counters
     w.sorted_pairs = o; o = align_up(o + sizeof(int32_t) * P);
     w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
     w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));
@@ -149,7 +149,7 @@ int cernels_moe_route(const int32_t* indices, int32_t T, int32_t K, int32_t E, i
     if (T > 0 && (!indices || !sorted_pairs)) return CERNELS_MOE_INVALID_ARGUMENT;
     if (workspace_bytes < cmoe::route_workspace_bytes(T, K, E)) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
     return hip_status(cmoe::launch_route(indices, T, K, E, tile_m, expert_offsets, sorted_pairs, tile_offsets,
-                                         tile_expert, meta, static_cast<int32_t*>(workspace), stream));
+                                         tile_expert, meta, static_cast<int32_t*>(workspace), nullptr, stream));
 }
 
 int cernels_moe_router(const void* x, const void* router_weight, const void* router_bias, int32_t T, int32_t H,

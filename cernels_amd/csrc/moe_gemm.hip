@@ -569,7 +569,7 @@ hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        hipStream_t stream);
+                        int32_t* sched, hipStream_t stream);
 
 // route -> gate_up GEMM -> down GEMM -> combine, all on stream s. Shapes were checked by the caller
 // (H % 64 == 0, F % 64 == 0, E <= 1024, T >= 1).
@@ -583,7 +583,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     mark(0);
     hipError_t st =
-        launch_route(idx, T, K, E, kBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts, s);
+        launch_route(idx, T, K, E, kBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts, nullptr, s);
     if (st != hipSuccess) return st;
     mark(1);
     const bool concat = layout == kLayoutConcat;

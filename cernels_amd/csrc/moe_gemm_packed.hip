@@ -144,6 +144,7 @@ struct PkParams {
     int bias_interleaved;          // GEMM1 bias order: 0 = [gate F | up F], 1 = gate/up interleaved
     int a_bytes;                   // GEMM1: bytes of x (< 2^31, checked by the caller)
     int fw;                        // fragments per item (<= kPkWaves); waves past fw idle
+    int* counters;                 // [8] per-XCD work counters, zeroed by the route kernel
 };
 
 // Word 3 of a raw buffer descriptor on gfx9-family GPUs (gfx950 included): 32-bit data format,
@@ -180,16 +181,23 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const int Kd = prm.Kd, nst = Kd / kBK;
     const int a_chunk = tid & 7;
 
-    // Items of XCD x are [x*per, x*per + per), handed to its slots in snake order (slot s takes
-    // s, 2*slots-1-s, 2*slots+s, ...) so that long and short items mix on every CU, while the items
-    // that share a weight tile (neighbours in the list) still run at the same time on one XCD.
-    auto item_of = [&](int j, WorkItem& w) {
-        const int off = (j & 1) ? (j + 1) * slots - 1 - slot : j * slots + slot;
-        const int it = xcd * per + off;
-        if (off >= per || it >= it_end) return false;
+    // Items of XCD x are [x*per, x*per + per), so that the items that share a weight tile
+    // (neighbours in the list) run at about the same time on one XCD's L2. Each slot of the XCD takes
+    // offsets s and 2*slots-1-s first (snake order: long and short items mix on every CU), then draws
+    // offsets 2*slots + n from the XCD's work counter: workgroups that run faster take more items,
+    // so the launch does not end on the slowest workgroup's fixed share. (Drawing from the other
+    // XCDs' counters once the own one is exhausted was measured slower: the blocking draws and the
+    // lost L2 sharing cost more than the balance gained.)
+    auto item_at = [&](int it, WorkItem& w) {  // it: global item index, or -1
+        if (it < 0) return false;
         w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
         return true;
     };
+    auto item_of_off = [&](int x, int off) {  // item at offset off of XCD x, or -1
+        const int it = x * per + off;
+        return (off < per && it < min(total, (x + 1) * per)) ? it : -1;
+    };
+    __shared__ int s_next;  // item after next (global index or -1), published once per item
     // Operands are read with buffer loads: a 128-bit descriptor per operand and item (uniform,
     // SGPRs) plus a 32-bit per-lane offset, so the k-loop holds no 64-bit addresses.
     //   A: GEMM1 gathers token rows of x (descriptor over all of x); GEMM2 reads the item's own
@@ -242,7 +250,12 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     };
 
     WorkItem cur;
-    if (!item_of(0, cur)) return;
+    if (!item_at(item_of_off(xcd, slot), cur)) return;
+    int it_nx = item_of_off(xcd, 2 * slots - 1 - slot);  // the next item
+    // Thread 0 holds the counter ticket of the item after next: drawn one item ahead, so the
+    // atomic's round trip is over long before its value is published.
+    int ticket = 0;
+    if (tid == 0) ticket = atomicAdd(prm.counters + xcd, 1);
     uint32_t a_cur[kPkMB / 2];  // activation row offsets of the current item
     __amdgpu_buffer_rsrc_t ra_cur = a_rsrc(cur), rb_cur = b_rsrc(cur);
     int bstep_cur = b_stride(cur);  // bytes between k-steps
@@ -295,7 +308,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     int par = 0;  // LDS buffer / weight slot of the current item's stage 0
     for (int j = 0;; ++j) {
         WorkItem nx;
-        const bool has_nx = item_of(j + 1, nx);
+        const bool has_nx = item_at(it_nx, nx);
         if (!has_nx) nx = cur;  // past the end the "next" loads re-read the current item
         const __amdgpu_buffer_rsrc_t ra_nx = a_rsrc(nx), rb_nx = b_rsrc(nx);
         const int bstep_nx = b_stride(nx);
@@ -444,6 +457,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         } else {
             dispatch(IC<0>{});
         }
+        if (tid == 0) s_next = item_of_off(xcd, 2 * slots + ticket);
 
         // ---- epilogue: element r of a transposed 32x32 accumulator block is row lane & 31 of the
         // block, column 8*(r/4) + 4*(lane/32) + (r%4) of the fragment. Only LDS reads and global
@@ -525,7 +539,11 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 }
             }
         }
-        if (!has_nx) break;
+        __syncthreads();  // s_next
+        const int it_nn = s_next;
+        if (!has_nx) break;  // tickets are drawn in increasing order: the held one is past the end too
+        it_nx = it_nn;
+        if (tid == 0) ticket = atomicAdd(prm.counters + xcd, 1);
         cur = nx;
         ra_cur = ra_nx;
         rb_cur = rb_nx;
@@ -568,7 +586,7 @@ static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s)
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        hipStream_t stream);
+                        int32_t* sched, hipStream_t stream);
 hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
                           hipStream_t s);
 
@@ -610,7 +628,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     mark(0);
     hipError_t st =
-        launch_route(idx, T, K, E, kPkBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts, s);
+        launch_route(idx, T, K, E, kPkBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts,
+                     meta + 8, s);
     if (st != hipSuccess) return st;
     mark(1);
     PkParams g1{};
@@ -634,6 +653,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.topk = K;
     g1.bias_interleaved = bias_interleaved;
     g1.a_bytes = T * H * 2;
+    g1.counters = meta + 8;
     if (act == kActSilu)
         st = b1 ? launch_pk_t<kModePkGateUp, kActSilu, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActSilu, false>(g1, max_tiles, s);
@@ -657,6 +677,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.NF = H / 32;
     g2.KS = F / 16;
     g2.fw = pick_fw((long long)T * K, E, g2.NF, F, pk_cu_count());
+    g2.counters = meta + 16;
     g2.n_tiles = ceil_div(g2.NF, g2.fw);
     st = b2 ? launch_pk_t<kModePkDown, kActSilu, true>(g2, max_tiles, s)
             : launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);

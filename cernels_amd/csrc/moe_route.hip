@@ -90,11 +90,16 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_count_kernel(const int32
     for (int i = tid; i < E; i += kRtThreads) counts[(long long)blockIdx.x * E + i] = h[i];
 }
 
+// Work counters of the grouped GEMMs that follow the route (zeroed here, so that no launch of its own
+// is needed): kSchedInts ints, or none when sched is null.
+constexpr int kSchedInts = 16;
+
 __global__ __launch_bounds__(kRouteThreads) void moe_route_scan_kernel(int32_t* __restrict__ counts, int ntiles, int E,
                                                                         int BM, int32_t* __restrict__ offsets,
                                                                         int32_t* __restrict__ tile_offsets,
                                                                         int32_t* __restrict__ tile_expert,
-                                                                        int32_t* __restrict__ meta) {
+                                                                        int32_t* __restrict__ meta,
+                                                                        int32_t* __restrict__ sched) {
     __shared__ int wave_tot[kRouteWaves];
     const int tid = threadIdx.x;
     const int e = tid;  // E <= kRouteThreads is checked on the host
@@ -124,6 +129,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_scan_kernel(int32_t* 
         meta[0] = tiles_total;
         meta[1] = valid_total;
     }
+    if (sched && tid < kSchedInts) sched[tid] = 0;
 }
 
 __global__ __launch_bounds__(kRtThreads) void moe_route_scatter_kernel(const int32_t* __restrict__ idx, int T, int K,
@@ -192,7 +198,7 @@ constexpr int kRtFusedCells = 28 * 1024;
 __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     const int32_t* __restrict__ idx, int T, int K, int E, int BM, int ntiles, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
-    int32_t* __restrict__ meta) {
+    int32_t* __restrict__ meta, int32_t* __restrict__ sched) {
     __shared__ int32_t h[kRtFusedCells];  // [ntiles][E]
     __shared__ int wave_tot[kRouteWaves];
     const int tid = threadIdx.x, P = T * K;  // P <= kRtFusedCells * kRtTile here, far below 2^31
@@ -256,6 +262,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
         meta[0] = tiles_total;
         meta[1] = valid_total;
     }
+    if (sched && tid < kSchedInts) sched[tid] = 0;
 }
 
 int route_tiles(int T, int K) { return ceil_div(T * K, kRtTile); }
@@ -263,16 +270,16 @@ size_t route_workspace_bytes(int T, int K, int E) { return (size_t)max(route_til
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        hipStream_t stream) {
+                        int32_t* sched, hipStream_t stream) {
     const int nt = route_tiles(T, K);
     if ((long long)nt * E <= kRtFusedCells) {
         hipLaunchKernelGGL(moe_route_count_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, idx, T, K, E, BM, nt,
-                           counts, offsets, tile_offsets, tile_expert, meta);
+                           counts, offsets, tile_offsets, tile_expert, meta, sched);
     } else {
         hipLaunchKernelGGL(moe_route_count_kernel, dim3(nt), dim3(kRtThreads), E * sizeof(int32_t), stream, idx, T, K,
                            E, counts);
         hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, counts, nt, E, BM, offsets,
-                           tile_offsets, tile_expert, meta);
+                           tile_offsets, tile_expert, meta, sched);
     }
     if (nt > 0)
         hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nt), dim3(kRtThreads), 4 * E * sizeof(int32_t), stream, idx,
