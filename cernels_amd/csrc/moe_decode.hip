@@ -264,30 +264,13 @@ static void launch_gateup_r(const uint16_t* x, const uint16_t* w1, const float* 
                        idx, glu, T, H, F, E, K);
 }
 
-// R (f per wave): 4 keeps 8 rows in flight per wave, but only if that still leaves about two
-// workgroups per CU when every pair picks a different expert; wide rows (MAXC > 4) use R = 2.
+// R (f per wave) = 2: four weight rows in flight per wave. Measured against R = 1 and R = 4 on both decode
+// workloads: R = 4 (eight rows, fewer and larger workgroups) was 2.5 us slower at T=8, H=1280 and
+// 1.4 us slower at T=1, H=2048; R = 1 was within noise of R = 2.
 template <int ACT, bool HAS_BIAS, int MAXC>
 static void launch_gateup_t(const uint16_t* x, const uint16_t* w1, const float* b1, const int32_t* idx, uint16_t* glu,
                             int T, int H, int F, int E, int K, hipStream_t s) {
-    const long long wgs_r4 = (long long)ceil_div(F, kDecWaves * 4) * min(T * K, E);
-    if (MAXC <= 4 && wgs_r4 >= 512)
-        launch_gateup_r<ACT, HAS_BIAS, MAXC, (MAXC <= 4 ? 4 : 2)>(x, w1, b1, idx, glu, T, H, F, E, K, s);
-    else
-        launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, T, H, F, E, K, s);
-}
-
-static int g_dec_cu_count = 0;
-
-static int dec_cu_count() {
-    if (g_dec_cu_count == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            g_dec_cu_count = n;
-        else
-            g_dec_cu_count = 256;
-    }
-    return g_dec_cu_count;
+    launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, T, H, F, E, K, s);
 }
 
 // Q (pairs in flight per wave) shrinks as rows widen, to bound the registers they take. Four
