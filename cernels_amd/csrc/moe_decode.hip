@@ -264,6 +264,20 @@ static void launch_gateup_r(const uint16_t* x, const uint16_t* w1, const float* 
                        idx, glu, T, H, F, E, K);
 }
 
+static int g_dec_cu_count = 0;
+
+static int dec_cu_count() {
+    if (g_dec_cu_count == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_dec_cu_count = n;
+        else
+            g_dec_cu_count = 256;
+    }
+    return g_dec_cu_count;
+}
+
 // R (f per wave) = 2: four weight rows in flight per wave. Measured against R = 1 and R = 4 on both decode
 // workloads: R = 4 (eight rows, fewer and larger workgroups) was 2.5 us slower at T=8, H=1280 and
 // 1.4 us slower at T=1, H=2048; R = 1 was within noise of R = 2.
