@@ -265,6 +265,113 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     if (sched && tid < kSchedInts) sched[tid] = 0;
 }
 
+// The whole route in one launch: workgroup b (1024 threads) owns route tile b. Every workgroup
+// builds all tiles' expert histograms in LDS and scans them (the same work as
+// moe_route_count_scan_kernel, repeated per workgroup: idx is small and L2-resident), which gives it
+// the absolute first write position of each expert in its own tile; workgroup 0 also writes the
+// offsets, tile list and counters. Then each of its 16 waves takes 64 consecutive pairs of the tile:
+// per-wave histograms give the write cursors, and lanes that share an expert are ranked with a
+// bit-sliced ballot, exactly as in the scatter kernel. Output identical to the two-launch route.
+constexpr int kRtOneCells = 39 * 1024;  // LDS cells: ntiles * E histograms + 16 * E wave cursors (156 KiB)
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
+    const int32_t* __restrict__ idx, int T, int K, int E, int BM, int ntiles, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
+    int32_t* __restrict__ meta, int32_t* __restrict__ sched) {
+    extern __shared__ int32_t rt_lds[];
+    int32_t* h = rt_lds;                    // [ntiles][E]
+    int32_t* wc = rt_lds + ntiles * E;      // [16][E] per-wave counts, then cursors
+    __shared__ int wave_tot[kRouteWaves];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), P = T * K;
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const float rT = 1.0f / (float)T;
+    for (int i = tid; i < (ntiles + kRouteWaves) * E; i += kRouteThreads) rt_lds[i] = 0;
+    const int q = blockIdx.x * kRtTile + w * kWave + lane;
+    const int eq = q < P ? expert_at(idx, q, T, K, E, rT) : -1;
+    __syncthreads();
+    const double rK = 1.0 / (double)K;
+    const int nchunks = ceil_div(P, 4);
+    for (int c0 = tid; c0 < nchunks; c0 += 8 * kRouteThreads) {
+        int ev[8][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = 4 * (c0 + u * kRouteThreads);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) ev[u][v] = i + v < P ? idx[i + v] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = 4 * (c0 + u * kRouteThreads);
+            if (i >= P) continue;
+            int t = (int)((double)i * rK), k = i - t * K;
+            t += (k >= K ? 1 : 0) - (k < 0 ? 1 : 0);
+            k = i - t * K;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int e = ev[u][v];
+                if ((unsigned)e < (unsigned)E) atomicAdd(&h[((k * T + t) / kRtTile) * E + e], 1);
+                if (++k == K) {
+                    k = 0;
+                    ++t;
+                }
+            }
+        }
+    }
+    if (eq >= 0) atomicAdd(&wc[w * E + eq], 1);
+    __syncthreads();
+    const int e = tid;  // E <= kRouteThreads is checked on the host
+    int run = 0, mine = 0;
+    if (e < E) {
+        for (int t = 0; t < ntiles; ++t) {
+            const int c = h[t * E + e];
+            if (t == (int)blockIdx.x) mine = run;
+            run += c;
+        }
+    }
+    int valid_total = 0, tiles_total = 0;
+    const int off = block_exclusive_scan(run, wave_tot, &valid_total);
+    const int nt = ceil_div(run, BM);
+    const int toff = block_exclusive_scan(nt, wave_tot, &tiles_total);
+    if (blockIdx.x == 0) {
+        if (e < E) {
+            offsets[e] = off;
+            tile_offsets[e] = toff;
+            for (int j = 0; j < nt; ++j) tile_expert[toff + j] = e;
+        }
+        if (tid == 0) {
+            offsets[E] = valid_total;
+            tile_offsets[E] = tiles_total;
+            meta[0] = tiles_total;
+            meta[1] = valid_total;
+        }
+        if (sched && tid < kSchedInts) sched[tid] = 0;
+    }
+    if (e < E) {
+        int cur = off + mine;
+#pragma unroll
+        for (int ww = 0; ww < kRouteWaves; ++ww) {
+            const int c = wc[ww * E + e];
+            wc[ww * E + e] = cur;
+            cur += c;
+        }
+    }
+    __syncthreads();
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+    const uint64_t lt_mask = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    const bool valid = eq >= 0;
+    uint64_t m = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = valid && ((eq >> b) & 1);
+        const uint64_t bb = __ballot(bit);
+        m &= bit ? bb : ~bb;
+    }
+    if (valid) {
+        const int k = div_by_t(q, T, rT), t = q - k * T;
+        sorted_pairs[wc[w * E + eq] + __popcll(m & lt_mask)] = t * K + k;
+    }
+}
+
 int route_tiles(int T, int K) { return ceil_div(T * K, kRtTile); }
 size_t route_workspace_bytes(int T, int K, int E) { return (size_t)max(route_tiles(T, K), 1) * E * sizeof(int32_t); }
 
@@ -272,6 +379,20 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
                         int32_t* sched, hipStream_t stream) {
     const int nt = route_tiles(T, K);
+    if (nt > 0 && (long long)(nt + kRouteWaves) * E <= kRtOneCells) {
+        static bool lds_attr = false;  // dynamic LDS above 64 KiB must be allowed once per process
+        if (!lds_attr) {
+            const hipError_t st = hipFuncSetAttribute((const void*)moe_route_one_kernel,
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                      kRtOneCells * (int)sizeof(int32_t));
+            if (st != hipSuccess) return st;
+            lds_attr = true;
+        }
+        hipLaunchKernelGGL(moe_route_one_kernel, dim3(nt), dim3(kRouteThreads),
+                           (size_t)(nt + kRouteWaves) * E * sizeof(int32_t), stream, idx, T, K, E, BM, nt, offsets,
+                           sorted_pairs, tile_offsets, tile_expert, meta, sched);
+        return hipGetLastError();
+    }
     if ((long long)nt * E <= kRtFusedCells) {
         hipLaunchKernelGGL(moe_route_count_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, idx, T, K, E, BM, nt,
                            counts, offsets, tile_offsets, tile_expert, meta, sched);
