@@ -91,6 +91,9 @@ SMALL = [
     (7, 1, 128, 64, 16, 8, "concat", "silu", False, 0, 0.0),
     (8, 1200, 256, 128, 64, 6, "concat", "silu", False, 0, 1.2),
     (9, 700, 576, 320, 3, 2, "concat", "silu", False, 0, 0.0),  # 20 and 18 fragments: idle waves in the last tile
+    # routes past the one-launch route's LDS limit (the GEMMs' work counters are then zeroed by the scan launch)
+    (10, 6000, 64, 64, 1024, 4, "concat", "silu", False, 5, 0.0),
+    (11, 8192, 64, 64, 1024, 8, "concat", "silu", False, 0, 1.0),
 ]
 
 

@@ -41,7 +41,10 @@ def test_route_golden(device, name):
 @pytest.mark.parametrize(
     "T,K,E,invalid",
     [(1, 1, 1, False), (1, 8, 128, False), (7, 3, 5, True), (333, 6, 64, True), (2048, 8, 128, False),
-     (4096, 10, 512, True), (5000, 4, 1024, False), (3, 2, 1024, True)],
+     (4096, 10, 512, True), (5000, 4, 1024, False), (3, 2, 1024, True),
+     # past the one-launch route's LDS limit ((tiles + 16) * E > 39 Ki cells): the count+scan and scatter
+     # launches, and above tiles * E > 28 Ki cells the separate count launch
+     (6000, 4, 1024, True), (8192, 8, 1024, False)],
 )
 def test_route_random(device, T, K, E, invalid):
     rng = np.random.default_rng(T * 31 + K * 7 + E)
