@@ -34,7 +34,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K,
                                  int bias_interleaved, int act, void* out, int32_t* offsets, int32_t* tile_offsets,
                                  int32_t* meta, int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts,
-                                 int max_tiles, uint16_t* glu, float* Y, hipStream_t s, hipEvent_t* ev);
+                                 int max_tiles, uint16_t* glu, float* Y, int8_t* yexp, hipStream_t s, hipEvent_t* ev);
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
                          const int32_t* idx, const float* route_w, uint16_t* glu, uint16_t* out, int T, int H, int F,
                          int E, int K, int act, hipStream_t s, hipEvent_t* ev);
@@ -49,7 +49,7 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct PrefillWs {
-    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, route_counts, glu, Y, total;
+    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, route_counts, glu, Y, yexp, total;
     int capacity;
 };
 
@@ -67,6 +67,7 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));
     w.glu = o;          o = align_up(o + sizeof(uint16_t) * P * F);
     w.Y = o;            o = align_up(o + sizeof(float) * P * H);
+    w.yexp = o;         o = align_up(o + (size_t)P * (H / 32));  // packed path: exponent per 32-column Y segment
     w.total = o;
     return w;
 }
@@ -247,7 +248,7 @@ int cernels_moe_experts_packed_staged(const void* x, const void* gate_up_packed,
         reinterpret_cast<int32_t*>(base + w.tile_offsets), reinterpret_cast<int32_t*>(base + w.meta),
         reinterpret_cast<int32_t*>(base + w.sorted_pairs), reinterpret_cast<int32_t*>(base + w.tile_expert),
         reinterpret_cast<int32_t*>(base + w.route_counts), w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
-        reinterpret_cast<float*>(base + w.Y), stream, stage_events));
+        reinterpret_cast<float*>(base + w.Y), reinterpret_cast<int8_t*>(base + w.yexp), stream, stage_events));
 }
 
 int cernels_moe_experts_packed(const void* x, const void* gate_up_packed, const float* gate_up_bias,

@@ -145,6 +145,7 @@ struct PkParams {
     int a_bytes;                   // GEMM1: bytes of x (< 2^31, checked by the caller)
     int fw;                        // fragments per item (<= kPkWaves); waves past fw idle
     int* counters;                 // [8] per-XCD work counters, zeroed by the route kernel
+    int8_t* yexp;                  // GEMM2: [P, H/32] exponent of each 32-column row segment of Y
 };
 
 // Word 3 of a raw buffer descriptor on gfx9-family GPUs (gfx950 included): 32-bit data format,
@@ -514,27 +515,46 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     }
                 }
             } else {
-                float* Y = reinterpret_cast<float*>(prm.out);
+                // Y row segments of 32 columns (this wave's fragment) in fp16 with a shared power-of-two
+                // exponent k: Y = fp16(y * 2^-k) * 2^k, k chosen so the segment's largest |y| scales
+                // below 2^14 (no fp16 overflow; rounding 2^-11 relative, vs 2^-8 for bf16). A row's two
+                // 16-column halves sit in lanes l and l ^ 32.
+                uint16_t* Yh = reinterpret_cast<uint16_t*>(prm.out);
+                const int NFH = prm.H / 32;
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
                     const int row = mb * 32 + (lane & 31);
+                    const int rc = min(row, kPkBM - 1);
+                    const float w = s_w[tb][rc];
+                    float a[16];
+                    float m = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        f32x4 bn = {0.f, 0.f, 0.f, 0.f};
+                        if constexpr (HAS_BIAS) bn = *reinterpret_cast<const f32x4*>(&s_bias[tb][32 * wave + 8 * i + c4]);
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) {
+                            float v = acc[mb][4 * i + jj];
+                            if constexpr (HAS_BIAS) v += bn[jj];
+                            a[4 * i + jj] = v * w;
+                            m = fmaxf(m, fabsf(a[4 * i + jj]));
+                        }
+                    }
+                    m = fmaxf(m, __shfl_xor(m, 32, kWave));
+                    const int k = max(-128, min(127, __builtin_amdgcn_frexp_expf(m) - 14));
                     if (row < rows) {
-                        const int p = s_pair[tb][row];
-                        const float w = s_w[tb][row];
+                        const long long p = s_pair[tb][row];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            f32x4 bn = {0.f, 0.f, 0.f, 0.f};
-                            if constexpr (HAS_BIAS) bn = *reinterpret_cast<const f32x4*>(&s_bias[tb][32 * wave + 8 * i + c4]);
-                            f32x4 v;
+                            uint32_t hb[4];
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj) {
-                                float a = acc[mb][4 * i + jj];
-                                if constexpr (HAS_BIAS) a += bn[jj];
-                                v[jj] = a * w;
-                            }
-                            *reinterpret_cast<f32x4*>(Y + (long long)p * prm.H + 32 * fc + 8 * i + c4) = v;
+                            for (int jj = 0; jj < 4; ++jj)
+                                hb[jj] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(a[4 * i + jj], -k));
+                            *reinterpret_cast<u32x2*>(Yh + p * prm.H + 32 * fc + 8 * i + c4) =
+                                u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
                         }
+                        if (lane < 32) prm.yexp[p * NFH + fc] = (int8_t)k;
                     }
                 }
             }
@@ -587,8 +607,32 @@ static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s)
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
                         int32_t* sched, hipStream_t stream);
-hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
-                          hipStream_t s);
+// out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] ), slots in k order, Y in the
+// fp16-with-segment-exponent form the packed down GEMM writes. One workgroup per token; a thread
+// owns 8 consecutive columns (one 16-byte load and one exponent per slot).
+__global__ __launch_bounds__(256) void moe_combine_h_kernel(const uint16_t* __restrict__ Yh,
+                                                            const int8_t* __restrict__ yexp,
+                                                            const int32_t* __restrict__ idx, uint16_t* __restrict__ out,
+                                                            int T, int K, int E, int H) {
+    const int t = blockIdx.x, NFH = H / 32;
+    for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < K; ++k) {
+            const int e = idx[t * K + k];
+            if ((unsigned)e >= (unsigned)E) continue;
+            const long long p = (long long)t * K + k;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(Yh + p * H + 8 * c);
+            const int ex = yexp[p * NFH + (8 * c) / 32];
+            auto h = [&](uint32_t w, int hi) {
+                return __builtin_amdgcn_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? w >> 16 : w & 0xffffu)), ex);
+            };
+            s0 += f32x4{h(v[0], 0), h(v[0], 1), h(v[1], 0), h(v[1], 1)};
+            s1 += f32x4{h(v[2], 0), h(v[2], 1), h(v[3], 0), h(v[3], 1)};
+        }
+        *reinterpret_cast<u32x4*>(out + (long long)t * H + 8 * c) =
+            u32x4{pack_bf16x2(s0[0], s0[1]), pack_bf16x2(s0[2], s0[3]), pack_bf16x2(s1[0], s1[1]), pack_bf16x2(s1[2], s1[3])};
+    }
+}
 
 int packed_tile_m() { return kPkBM; }
 
@@ -624,7 +668,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K,
                                  int bias_interleaved, int act, void* out, int32_t* offsets, int32_t* tile_offsets,
                                  int32_t* meta, int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts,
-                                 int max_tiles, uint16_t* glu, float* Y, hipStream_t s, hipEvent_t* ev) {
+                                 int max_tiles, uint16_t* glu, float* Y, int8_t* yexp, hipStream_t s,
+                                 hipEvent_t* ev) {
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     mark(0);
     hipError_t st =
@@ -672,7 +717,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.A = glu;
     g2.B = static_cast<const uint16_t*>(w2p);
     g2.bias = b2;
-    g2.out = Y;
+    g2.out = Y;  // written as fp16 row segments (half of the fp32 buffer) with exponents in yexp
+    g2.yexp = yexp;
     g2.Kd = F;
     g2.NF = H / 32;
     g2.KS = F / 16;
@@ -683,7 +729,9 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
             : launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(3);
-    st = launch_combine(Y, idx, static_cast<uint16_t*>(out), T, K, E, H, s);
+    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(256), 0, s, reinterpret_cast<const uint16_t*>(Y), yexp, idx,
+                       static_cast<uint16_t*>(out), T, K, E, H);
+    st = hipGetLastError();
     mark(4);
     return st;
 }
