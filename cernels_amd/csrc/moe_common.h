@@ -21,6 +21,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+// Word 3 of a raw buffer descriptor on gfx9-family GPUs (gfx950 included): 32-bit data format,
+// no swizzle, no index stride. Loads past num_records return 0 without a memory access.
+constexpr int kBufferWord3 = 0x00020000;
+
 // Weight layouts (mirrors include/cernels_moe.h).
 constexpr int kLayoutConcat = 0;       // gate_up [E, 2F, H] (gate rows, then up rows), down [E, H, F]
 constexpr int kLayoutInterleaved = 1;  // gate_up [E, H, 2F] (even col gate, odd col up), down [E, F, H]

@@ -148,9 +148,6 @@ struct PkParams {
     int8_t* yexp;                  // GEMM2: [P, H/32] exponent of each 32-column row segment of Y
 };
 
-// Word 3 of a raw buffer descriptor on gfx9-family GPUs (gfx950 included): 32-bit data format,
-// no swizzle, no index stride.
-constexpr int kBufferWord3 = 0x00020000;
 
 template <int N>
 using IC = std::integral_constant<int, N>;

@@ -272,6 +272,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
 // offsets, tile list and counters. Then each of its 16 waves takes 64 consecutive pairs of the tile:
 // per-wave histograms give the write cursors, and lanes that share an expert are ranked with a
 // bit-sliced ballot, exactly as in the scatter kernel. Output identical to the two-launch route.
+constexpr int kRtChunks = 8;           // 16-byte idx chunks per thread and round of the histogram pass
 constexpr int kRtOneCells = 39 * 1024;  // LDS cells: ntiles * E histograms + 16 * E wave cursors (156 KiB)
 
 __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
@@ -291,16 +292,17 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     __syncthreads();
     const double rK = 1.0 / (double)K;
     const int nchunks = ceil_div(P, 4);
-    for (int c0 = tid; c0 < nchunks; c0 += 8 * kRouteThreads) {
-        int ev[8][4];
+    // idx in 16-byte chunks through a buffer descriptor (P * 4 < 2^31 on this path): one load
+    // instruction per chunk, the tail of the last chunk reads 0 and is masked by i + v < P
+    const __amdgpu_buffer_rsrc_t ridx = __builtin_amdgcn_make_buffer_rsrc((void*)idx, (short)0, P * 4, kBufferWord3);
+    for (int c0 = tid; c0 < nchunks; c0 += kRtChunks * kRouteThreads) {
+        u32x4 ev[kRtChunks];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int i = 4 * (c0 + u * kRouteThreads);
+        for (int u = 0; u < kRtChunks; ++u)
+            ev[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  ridx, (uint32_t)(c0 + u * kRouteThreads) * 16u, 0, 0));
 #pragma unroll
-            for (int v = 0; v < 4; ++v) ev[u][v] = i + v < P ? idx[i + v] : -1;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kRtChunks; ++u) {
             const int i = 4 * (c0 + u * kRouteThreads);
             if (i >= P) continue;
             int t = (int)((double)i * rK), k = i - t * K;
@@ -308,8 +310,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
             k = i - t * K;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int e = ev[u][v];
-                if ((unsigned)e < (unsigned)E) atomicAdd(&h[((k * T + t) / kRtTile) * E + e], 1);
+                const int e = (int)ev[u][v];
+                if (i + v < P && (unsigned)e < (unsigned)E) atomicAdd(&h[((k * T + t) / kRtTile) * E + e], 1);
                 if (++k == K) {
                     k = 0;
                     ++t;
