@@ -54,6 +54,27 @@ def test_route_random(device, T, K, E, invalid):
         _assert_same(_gpu_route(idx, E, device, tile_m), O.route_reference(idx, E, tile_m))
 
 
+@pytest.mark.parametrize("T,K,E,shift", [(333, 6, 64, 1), (2047, 3, 128, 3), (4095, 10, 512, 2)])
+def test_route_unaligned_indices(device, T, K, E, shift):
+    """indices starting 4*shift bytes into an allocation (a contiguous slice), T*K not a multiple of 4:
+    the histogram pass reads idx in 16-byte chunks whatever the pointer's alignment and masks the tail."""
+    from cernels_amd import ops
+
+    rng = np.random.default_rng(T + 17 * shift)
+    idx = rng.integers(-2, E + 2, size=(T, K))
+    buf = torch.zeros(T * K + shift, dtype=torch.int32, device=device)
+    d = buf[shift:].view(T, K)
+    d.copy_(torch.as_tensor(idx, dtype=torch.int32))
+    assert d.data_ptr() % 16 != 0 and d.is_contiguous()
+    offs, pairs, toff, texp, meta = ops.route(d, E, 128)
+    torch.cuda.synchronize()
+    m = meta.cpu().numpy()
+    got = dict(offsets=offs.cpu().numpy(), sorted_pairs=pairs.cpu().numpy()[: int(m[1])],
+               tile_offsets=toff.cpu().numpy(), tile_expert=texp.cpu().numpy()[: int(m[0])],
+               num_tiles=int(m[0]), num_valid=int(m[1]))
+    _assert_same(got, O.route_reference(idx, E, 128))
+
+
 def test_route_skewed_single_expert(device):
     idx = np.zeros((4096, 10), dtype=np.int64)  # every pair on expert 0
     idx[::7, 3] = 511
