@@ -379,6 +379,11 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 for (int k = 0; k < R; ++k) af[k] = read_af(k / NMB, k % NMB);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
+                    // Raised wave priority for the k-step's MFMA group: while the other wave of the SIMD is
+                    // in its step's non-MFMA part (first LDS reads, LDS writes, barrier), the wave that has
+                    // MFMAs to issue wins the arbitration, which keeps the shared matrix unit fed.
+                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_s_setprio(1);
                     __builtin_amdgcn_sched_barrier(0);
                     const bf16x8 bq = __builtin_bit_cast(bf16x8, breg[b][q]);
 #pragma unroll
@@ -399,6 +404,8 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                         if (q * NMB + mb + R < NK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
                     }
                     if (KIND == 0 || XPF) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_s_setprio(0);
                 }
                 } else if constexpr (KIND != 0 && XPF) {
                     // An idle wave may be active in the next item: its first two weight stages are
