@@ -80,53 +80,75 @@ __device__ __forceinline__ void wave_reduce_groups(float (&v)[N], int lane) {
 // glu[p, f] = bf16(act(x[t_p] . W1_e[f] + b1_e[f], x[t_p] . W1_e[F+f] + b1_e[F+f])) for the pairs p
 // of one distinct expert e.
 // grid: (ceil(F / (4 * R)), min(T*K, E)); blockIdx.y = u picks the u-th smallest distinct expert
-// (workgroups past the number of distinct experts return at once). Wave w owns R consecutive f and
-// keeps their 2R weight rows in registers for all of e's pairs.
+// (waves past the number of distinct experts return at once). Wave w owns R consecutive f and
+// keeps their 2R weight rows in registers for all of e's pairs. Every wave finds e and its pairs
+// on its own (its own LDS bitmap and pair list, ballots, no workgroup barrier), loads the first
+// pair's x row ahead of its weight rows and each further pair's x row while the previous pair is
+// reduced. Measured against one workgroup-wide selection (two barriers, x row loaded per pair):
+// same output bit for bit, 29.9 -> 28.9 us at T=8 (H=1280) and 10.6 -> 10.3 us at T=1 (H=2048).
 template <int ACT, bool HAS_BIAS, int MAXC, int R>
 __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1, const float* __restrict__ b1,
     const int32_t* __restrict__ idx, uint16_t* __restrict__ glu, int T, int H, int F, int E, int K) {
-    __shared__ uint32_t bits[kDecMaxExperts / 32];
-    __shared__ int s_e, s_np;
-    __shared__ int s_wcnt[kDecWaves];
-    __shared__ int s_pairs[kDecMaxPairs];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    __shared__ uint32_t bits[kDecWaves][kDecMaxExperts / 32];
+    __shared__ int plist[kDecWaves][kDecMaxPairs];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int P = T * K, u = blockIdx.y;
-
-    // ---- which expert: the u-th set bit of the bitmap of valid expert ids
-    if (tid < kDecMaxExperts / 32) bits[tid] = 0u;
-    int ep = -1;
-    if (tid < P) {  // P <= 256 is checked on the host
-        const int v = idx[tid];
-        ep = ((unsigned)v < (unsigned)E) ? v : -1;
-    }
-    __syncthreads();
-    if (ep >= 0) atomicOr(&bits[ep >> 5], 1u << (ep & 31));
-    __syncthreads();
-    if (wave == 0) {
-        uint32_t w = lane < kDecMaxExperts / 32 ? bits[lane] : 0u;
-        const int c = __popc(w);
-        int incl = c;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int y = __shfl_up(incl, o, kWave);
-            if (lane >= o) incl += y;
-        }
-        const int excl = incl - c;
-        if (lane == 0) s_e = -1;
-        __builtin_amdgcn_wave_barrier();
-        if (u >= excl && u < incl) {  // at most one lane
-            for (int r = u - excl; r > 0; --r) w &= w - 1;
-            s_e = lane * 32 + __ffs(w) - 1;
-        }
-    }
-    __syncthreads();
-    const int e = s_e;
-    if (e < 0) return;  // uniform: fewer distinct experts than u + 1
-
-    // ---- start streaming this wave's 2R weight rows before building the pair list
-    const int nch = H / 8;
     const int f0 = (blockIdx.x * kDecWaves + wave) * R;
+    if (f0 >= F) return;  // wave-uniform; nothing below synchronises the workgroup
+
+    // ---- the pairs' expert ids, four 64-pair chunks (P <= 256 is checked on the host)
+    int ev[kDecMaxPairs / kWave];
+#pragma unroll
+    for (int c = 0; c < kDecMaxPairs / kWave; ++c) {
+        const int p = lane + kWave * c;
+        const int v = p < P ? idx[p] : -1;
+        ev[c] = ((unsigned)v < (unsigned)E) ? v : -1;
+    }
+    // ---- this wave's bitmap of valid expert ids (its own LDS words; LDS ops of a wave run in order)
+    uint32_t* wb = bits[wave];
+    if (lane < kDecMaxExperts / 32) wb[lane] = 0u;
+#pragma unroll
+    for (int c = 0; c < kDecMaxPairs / kWave; ++c)
+        if (ev[c] >= 0) atomicOr(&wb[ev[c] >> 5], 1u << (ev[c] & 31));
+    uint32_t bw = lane < kDecMaxExperts / 32 ? wb[lane] : 0u;
+    const int cnt = __popc(bw);
+    int incl = cnt;
+#pragma unroll
+    for (int o = 1; o < kDecMaxExperts / 32; o <<= 1) {
+        const int y = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += y;
+    }
+    const int excl = incl - cnt;
+    const bool holder = u >= excl && u < incl;  // at most one lane
+    int eh = 0;
+    if (holder) {
+        for (int r = u - excl; r > 0; --r) bw &= bw - 1;
+        eh = lane * 32 + __ffs(bw) - 1;
+    }
+    const uint64_t hb = __ballot(holder);
+    if (hb == 0ull) return;  // fewer distinct experts than u + 1
+    const int e = __builtin_amdgcn_readlane(eh, __ffsll((unsigned long long)hb) - 1);
+
+    // ---- pairs of e, ascending p, into this wave's list
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    int np = 0;
+#pragma unroll
+    for (int c = 0; c < kDecMaxPairs / kWave; ++c) {
+        const bool mine = ev[c] == e;
+        const uint64_t mk = __ballot(mine);
+        if (mine) plist[wave][np + __popcll(mk & lt)] = kWave * c + lane;
+        np += __popcll(mk);
+    }
+    int ip = 0;
+    auto pop = [&]() -> int { return ip < np ? __builtin_amdgcn_readfirstlane(plist[wave][ip++]) : -1; };
+    const int nch = H / 8;
+    int p = pop();
+    u32x4 xs[2][MAXC];
+    load_row<MAXC>(x + (long long)(p / K) * H, nch, lane, xs[0]);
+
+    // ---- this wave's 2R weight rows
     const uint16_t* we = w1 + (long long)e * 2 * F * H;
     u32x4 wr[2 * R][MAXC];  // rows: gate f0, up f0, gate f0+1, up f0+1, ...
 #pragma unroll
@@ -135,22 +157,9 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
         load_row<MAXC>(we + (long long)f * H, nch, lane, wr[2 * r]);
         load_row<MAXC>(we + (long long)(F + f) * H, nch, lane, wr[2 * r + 1]);
     }
+    int pn = pop();
+    if (pn >= 0) load_row<MAXC>(x + (long long)(pn / K) * H, nch, lane, xs[1]);
 
-    // ---- pairs of e, ascending p
-    const bool mine = ep == e;
-    const uint64_t ball = __ballot(mine);
-    if (lane == 0) s_wcnt[wave] = __popcll(ball);
-    __syncthreads();
-    int base = 0;
-#pragma unroll
-    for (int w = 0; w < kDecWaves; ++w) base += w < wave ? s_wcnt[w] : 0;
-    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-    if (mine) s_pairs[base + __popcll(ball & lt)] = tid;
-    if (tid == 0) s_np = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
-    __syncthreads();
-    if (f0 >= F) return;
-
-    // after the reduction, lane group r (the upper log2(R) lane bits) holds the gate/up sums of f0 + r
     constexpr int gr_shift = 6 - (R == 1 ? 0 : (R == 2 ? 1 : (R == 4 ? 2 : 3)));
     const int my_r = lane >> gr_shift;
     float bg = 0.f, bu = 0.f;
@@ -160,21 +169,29 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
         bu = b1[(long long)e * 2 * F + F + f];
     }
     const bool writer = (lane & ((1 << gr_shift) - 1)) == 0 && f0 + my_r < F;
-    const int np = s_np;
-    for (int s = 0; s < np; ++s) {
-        const int p = s_pairs[s];
-        const int t = p / K;
-        u32x4 xv[MAXC];
-        load_row<MAXC>(x + (long long)t * H, nch, lane, xv);
+    auto emit = [&](int pp, auto bc) {
+        constexpr int B = decltype(bc)::value;
         float v[2 * R];
 #pragma unroll
         for (int j = 0; j < 2 * R; ++j) {
             v[j] = 0.f;
 #pragma unroll
-            for (int i = 0; i < MAXC; ++i) v[j] = dot8(wr[j][i], xv[i], v[j]);
+            for (int i = 0; i < MAXC; ++i) v[j] = dot8(wr[j][i], xs[B][i], v[j]);
         }
         wave_reduce_groups<2 * R, 2>(v, lane);
-        if (writer) glu[(long long)p * F + f0 + my_r] = f32_to_bf16_bits(swiglu<ACT>(v[0] + bg, v[1] + bu));
+        if (writer) glu[(long long)pp * F + f0 + my_r] = f32_to_bf16_bits(swiglu<ACT>(v[0] + bg, v[1] + bu));
+    };
+    for (;;) {
+        emit(p, std::integral_constant<int, 0>{});
+        if (pn < 0) break;
+        p = pn;
+        pn = pop();
+        if (pn >= 0) load_row<MAXC>(x + (long long)(pn / K) * H, nch, lane, xs[0]);
+        emit(p, std::integral_constant<int, 1>{});
+        if (pn < 0) break;
+        p = pn;
+        pn = pop();
+        if (pn >= 0) load_row<MAXC>(x + (long long)(pn / K) * H, nch, lane, xs[1]);
     }
 }
 
