@@ -36,8 +36,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  int32_t* meta, int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts,
                                  int max_tiles, uint16_t* glu, float* Y, int8_t* yexp, hipStream_t s, hipEvent_t* ev);
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
-                         const int32_t* idx, const float* route_w, uint16_t* glu, uint16_t* out, int T, int H, int F,
-                         int E, int K, int act, hipStream_t s, hipEvent_t* ev);
+                         const int32_t* idx, const float* route_w, uint16_t* glu, int32_t* order, uint16_t* out,
+                         int T, int H, int F, int E, int K, int act, hipStream_t s, hipEvent_t* ev);
 }  // namespace cmoe
 
 namespace {
@@ -73,7 +73,7 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
 }
 
 struct DecodeWs {
-    size_t glu, total;
+    size_t glu, order, total;
 };
 
 DecodeWs decode_ws(int T, int H, int F, int K) {
@@ -82,6 +82,7 @@ DecodeWs decode_ws(int T, int H, int F, int K) {
     const long long P = (long long)T * K;
     size_t o = 0;
     w.glu = o; o = align_up(o + sizeof(uint16_t) * P * F);
+    w.order = o; o = align_up(o + sizeof(int32_t) * P);  // valid pairs sorted by expert, then -1
     w.total = o;
     return w;
 }
@@ -336,7 +337,8 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
     return hip_status(cmoe::launch_decode(
         static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(gate_up_proj), gate_up_bias,
         static_cast<const uint16_t*>(down_proj), down_bias, indices, weights,
-        reinterpret_cast<uint16_t*>(base + w.glu), static_cast<uint16_t*>(out), T, H, F, E, K, act, stream,
+        reinterpret_cast<uint16_t*>(base + w.glu), reinterpret_cast<int32_t*>(base + w.order),
+        static_cast<uint16_t*>(out), T, H, F, E, K, act, stream,
         stage_events));
 }
 

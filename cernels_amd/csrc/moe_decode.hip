@@ -89,7 +89,8 @@ __device__ __forceinline__ void wave_reduce_groups(float (&v)[N], int lane) {
 template <int ACT, bool HAS_BIAS, int MAXC, int R>
 __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1, const float* __restrict__ b1,
-    const int32_t* __restrict__ idx, uint16_t* __restrict__ glu, int T, int H, int F, int E, int K) {
+    const int32_t* __restrict__ idx, uint16_t* __restrict__ glu, int32_t* __restrict__ order, int T, int H, int F,
+    int E, int K) {
     __shared__ uint32_t bits[kDecWaves][kDecMaxExperts / 32];
     __shared__ int plist[kDecWaves][kDecMaxPairs];
     const int lane = threadIdx.x & (kWave - 1);
@@ -105,6 +106,17 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
         const int p = lane + kWave * c;
         const int v = p < P ? idx[p] : -1;
         ev[c] = ((unsigned)v < (unsigned)E) ? v : -1;
+    }
+    // Wave 0 of the first row group of each expert publishes that expert's pairs in the pair order the down
+    // GEMV walks (by expert, then by pair); the one of expert 0 also marks the entries past the valid pairs.
+    const bool lead = blockIdx.x == 0 && wave == 0;
+    if (lead && u == 0) {
+        int nv = 0;
+#pragma unroll
+        for (int c = 0; c < kDecMaxPairs / kWave; ++c) nv += __popcll(__ballot(ev[c] >= 0));
+#pragma unroll
+        for (int c = 0; c < kDecMaxPairs / kWave; ++c)
+            if (nv + lane + kWave * c < P) order[nv + lane + kWave * c] = -1;
     }
     // ---- this wave's bitmap of valid expert ids (its own LDS words; LDS ops of a wave run in order)
     uint32_t* wb = bits[wave];
@@ -133,12 +145,20 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
 
     // ---- pairs of e, ascending p, into this wave's list
     const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-    int np = 0;
+    int np = 0, base = 0;  // base: valid pairs of smaller expert ids (lead wave only)
+    if (lead) {
+#pragma unroll
+        for (int c = 0; c < kDecMaxPairs / kWave; ++c) base += __popcll(__ballot(ev[c] >= 0 && ev[c] < e));
+    }
 #pragma unroll
     for (int c = 0; c < kDecMaxPairs / kWave; ++c) {
         const bool mine = ev[c] == e;
         const uint64_t mk = __ballot(mine);
-        if (mine) plist[wave][np + __popcll(mk & lt)] = kWave * c + lane;
+        if (mine) {
+            const int at = np + __popcll(mk & lt);
+            plist[wave][at] = kWave * c + lane;
+            if (lead) order[base + at] = (e << 16) | (kWave * c + lane);
+        }
         np += __popcll(mk);
     }
     int ip = 0;
@@ -196,66 +216,95 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
 }
 
 // out[t, h] = bf16( sum over valid slots k of w_{t,k} * (glu[t*K+k] . W2_{e}[h] + b2_e[h]) ).
-// grid: ceil(H / HB), 8 waves; HB = 4 output rows per workgroup while that still leaves two
-// workgroups per CU and rows are short (F <= 1024), else 2. Wave w takes the pairs p = w, w+8, ..., Q at a time (all Q pairs'
-// weight rows and glu rows in flight together), accumulating per (token, row) in the lane that
-// holds the token; the eight waves' partial sums are added in wave order at the end, so the result
-// does not depend on timing. Pair indices are wave-uniform, so expert ids and routing weights come
-// through the scalar cache.
-template <bool HAS_BIAS, int MAXC, int Q, int HB>
+// grid: ceil(H / HB), 8 waves; HB = 4 output rows per workgroup while that still leaves two workgroups per CU
+// and rows are short (F <= 1024), else 2. The valid pairs, sorted by expert and then by pair (order[P], written by
+// the gate_up launch; -1 past the valid pairs), are cut into eight consecutive runs, one per wave. A wave walks
+// its run QB pairs at a time (all their down rows and glu rows in flight together) and loads an expert's rows
+// only where the expert changes: consecutive pairs of one expert reuse the rows already in registers. Each lane
+// accumulates the sums of the token it holds; the eight waves' partial sums are added in wave order at the end,
+// so the result does not depend on timing. Run entries are wave-uniform (scalar loads).
+template <bool HAS_BIAS, int MAXC, int QB, int HB>
 __global__ __launch_bounds__(kDnThreads) void moe_decode_down_kernel(
     const uint16_t* __restrict__ glu, const uint16_t* __restrict__ w2, const float* __restrict__ b2,
-    const int32_t* __restrict__ idx, const float* __restrict__ route_w, uint16_t* __restrict__ out, int T, int H,
-    int F, int E, int K) {
+    const int32_t* __restrict__ order, const float* __restrict__ route_w, uint16_t* __restrict__ out, int T, int H,
+    int F, int K) {
+    static_assert(QB == 1 || QB == 2, "pairs per batch");
     __shared__ float part[kDnWaves][HB][kDecMaxTokens];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int h0 = blockIdx.x * HB;
     const int nch = F / 8, P = T * K;
+    const int run = ceil_div(P, kDnWaves);
+    const int i0 = wave * run, i1 = min(i0 + run, P);
     float acc[HB];
 #pragma unroll
     for (int j = 0; j < HB; ++j) acc[j] = 0.f;  // lane t holds token t's sums
 
-    for (int p0 = wave; p0 < P; p0 += Q * kDnWaves) {
-        int pp[Q], ee[Q];
+    u32x4 wr[QB][HB][MAXC], gv[QB][MAXC];
+    auto rows = [&](int e, auto sc) {
+        constexpr int S = decltype(sc)::value;
+        const uint16_t* we = w2 + (long long)e * H * F;
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            pp[q] = p0 + q * kDnWaves;
-            const int v = pp[q] < P ? idx[pp[q]] : -1;
-            ee[q] = ((unsigned)v < (unsigned)E) ? v : -1;
-        }
-        u32x4 wr[Q][HB][MAXC], gv[Q][MAXC];
+        for (int j = 0; j < HB; ++j) load_row<MAXC>(we + (long long)min(h0 + j, H - 1) * F, nch, lane, wr[S][j]);
+    };
+    int prev_e = -1, prev_slot = 0;  // expert whose rows the registers hold, and in which slot
+    for (int i = i0; i < i1; i += QB) {
+        const int o0 = order[i];
+        if (o0 < 0) break;  // past the valid pairs (wave-uniform)
+        const int o1r = QB == 2 && i + 1 < i1 ? order[i + 1] : -1;
+        const bool two = o1r >= 0;  // wave-uniform
+        const int o1 = two ? o1r : o0;
+        const int e0 = o0 >> 16, p0 = o0 & 0xffff, e1 = o1 >> 16, p1 = o1 & 0xffff;
+        if (e0 != prev_e) rows(e0, std::integral_constant<int, 0>{});
+        else if constexpr (QB == 2) {
+            if (prev_slot == 1) {
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            if (ee[q] >= 0) {
-                const uint16_t* we = w2 + (long long)ee[q] * H * F;
+                for (int j = 0; j < HB; ++j)
 #pragma unroll
-                for (int j = 0; j < HB; ++j) load_row<MAXC>(we + (long long)min(h0 + j, H - 1) * F, nch, lane, wr[q][j]);
-                load_row<MAXC>(glu + (long long)pp[q] * F, nch, lane, gv[q]);
+                    for (int c = 0; c < MAXC; ++c) wr[0][j][c] = wr[QB - 1][j][c];
             }
         }
+        const bool same = e1 == e0;
+        if constexpr (QB == 2) {
+            if (!same) rows(e1, std::integral_constant<int, QB - 1>{});
+        }
+        load_row<MAXC>(glu + (long long)p0 * F, nch, lane, gv[0]);
+        if constexpr (QB == 2) {
+            load_row<MAXC>(glu + (long long)p1 * F, nch, lane, gv[QB - 1]);
+            if (same) {  // after the glu loads are issued: the copy waits for the rows only
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            if (ee[q] < 0) continue;  // wave-uniform
-            float d[HB];
+                for (int j = 0; j < HB; ++j)
+#pragma unroll
+                    for (int c = 0; c < MAXC; ++c) wr[QB - 1][j][c] = wr[0][j][c];
+            }
+        }
+        float d[QB * HB];
+#pragma unroll
+        for (int q = 0; q < QB; ++q)
 #pragma unroll
             for (int j = 0; j < HB; ++j) {
-                d[j] = 0.f;
+                d[q * HB + j] = 0.f;
 #pragma unroll
-                for (int i = 0; i < MAXC; ++i) d[j] = dot8(wr[q][j][i], gv[q][i], d[j]);
+                for (int c = 0; c < MAXC; ++c) d[q * HB + j] = dot8(wr[q][j][c], gv[q][c], d[q * HB + j]);
             }
-            wave_reduce_groups<HB, 1>(d, lane);  // row j's total sits in lanes [j*64/HB, (j+1)*64/HB)
-            const float wp = route_w[pp[q]];
-            const int t = pp[q] / K;
+        wave_reduce_groups<QB * HB, 1>(d, lane);  // value v's total sits in lanes [v*64/(QB*HB), ...)
+#pragma unroll
+        for (int q = 0; q < QB; ++q) {
+            if (q == 1 && !two) break;  // wave-uniform
+            const int pp = q == 0 ? p0 : p1, ee = q == 0 ? e0 : e1;
+            const float wp = route_w[pp];
+            const int t = pp / K;
 #pragma unroll
             for (int j = 0; j < HB; ++j) {
                 const float dj = __builtin_bit_cast(
-                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d[0]), j * (kWave / HB)));
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, d[0]), (q * HB + j) * (kWave / (QB * HB))));
                 float bj = 0.f;
-                if constexpr (HAS_BIAS) bj = b2[(long long)ee[q] * H + min(h0 + j, H - 1)];
+                if constexpr (HAS_BIAS) bj = b2[(long long)ee * H + min(h0 + j, H - 1)];
                 if (lane == t) acc[j] += wp * (dj + bj);
             }
         }
+        prev_e = two ? e1 : e0;
+        prev_slot = two ? 1 : 0;
     }
 #pragma unroll
     for (int j = 0; j < HB; ++j) part[wave][j][lane] = acc[j];
@@ -275,10 +324,10 @@ int decode_max_tokens() { return kDecMaxTokens; }
 
 template <int ACT, bool HAS_BIAS, int MAXC, int R>
 static void launch_gateup_r(const uint16_t* x, const uint16_t* w1, const float* b1, const int32_t* idx, uint16_t* glu,
-                            int T, int H, int F, int E, int K, hipStream_t s) {
+                            int32_t* order, int T, int H, int F, int E, int K, hipStream_t s) {
     dim3 grid(ceil_div(F, kDecWaves * R), min(T * K, E));
     hipLaunchKernelGGL((moe_decode_gateup_kernel<ACT, HAS_BIAS, MAXC, R>), grid, dim3(kDecThreads), 0, s, x, w1, b1,
-                       idx, glu, T, H, F, E, K);
+                       idx, glu, order, T, H, F, E, K);
 }
 
 static int g_dec_cu_count = 0;
@@ -300,29 +349,33 @@ static int dec_cu_count() {
 // 1.4 us slower at T=1, H=2048; R = 1 was within noise of R = 2.
 template <int ACT, bool HAS_BIAS, int MAXC>
 static void launch_gateup_t(const uint16_t* x, const uint16_t* w1, const float* b1, const int32_t* idx, uint16_t* glu,
-                            int T, int H, int F, int E, int K, hipStream_t s) {
-    launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, T, H, F, E, K, s);
+                            int32_t* order, int T, int H, int F, int E, int K, hipStream_t s) {
+    launch_gateup_r<ACT, HAS_BIAS, MAXC, 2>(x, w1, b1, idx, glu, order, T, H, F, E, K, s);
 }
 
-// Q (pairs in flight per wave) shrinks as rows widen, to bound the registers they take. Four
-// output rows per workgroup (with two pairs in flight) when H / 4 still fills every CU twice:
-// fewer, larger workgroups stream the same rows with less per-workgroup overhead.
+// QB (pairs per batch) is 2 while rows are short (F <= 2048) and a wave has more than one pair, else 1, to bound
+// the registers they take. Four output rows per workgroup when H / 4 still fills every CU twice: fewer, larger
+// workgroups stream the same rows with less per-workgroup overhead. With two rows, two pairs per batch keep
+// three workgroups per CU resident, so T=8's 640 workgroups (H=1280) run in one wave of residency.
+template <bool HAS_BIAS, int MAXC, int QB, int HB>
+static void launch_down_k(const uint16_t* glu, const uint16_t* w2, const float* b2, const int32_t* order,
+                          const float* route_w, uint16_t* out, int T, int H, int F, int K, hipStream_t s) {
+    hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, QB, HB>), dim3(ceil_div(H, HB)), dim3(kDnThreads), 0, s,
+                       glu, w2, b2, order, route_w, out, T, H, F, K);
+}
 template <bool HAS_BIAS, int MAXC>
-static void launch_down_t(const uint16_t* glu, const uint16_t* w2, const float* b2, const int32_t* idx,
-                          const float* route_w, uint16_t* out, int T, int H, int F, int E, int K, hipStream_t s) {
+static void launch_down_t(const uint16_t* glu, const uint16_t* w2, const float* b2, const int32_t* order,
+                          const float* route_w, uint16_t* out, int T, int H, int F, int K, hipStream_t s) {
+    const bool one = T * K <= kDnWaves;  // at most one pair per wave
     if constexpr (MAXC <= 2) {
         if (H / 4 >= 2 * dec_cu_count()) {
-            hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, 2, 4>), dim3(ceil_div(H, 4)), dim3(kDnThreads), 0,
-                               s, glu, w2, b2, idx, route_w, out, T, H, F, E, K);
+            if (one) launch_down_k<HAS_BIAS, MAXC, 1, 4>(glu, w2, b2, order, route_w, out, T, H, F, K, s);
+            else launch_down_k<HAS_BIAS, MAXC, 2, 4>(glu, w2, b2, order, route_w, out, T, H, F, K, s);
             return;
         }
     }
-    // Two rows per workgroup: at 16-byte chunks of F <= 1024 (MAXC = 2), two pairs in flight per wave keep the
-    // kernel at 62 VGPRs, so three workgroups fit per CU and T=8's 640 workgroups (H=1280) run in one wave of
-    // residency; four pairs need 110 VGPRs (two per CU): 21.5 against 20.6 us, same output bit for bit.
-    constexpr int Q = MAXC == 1 ? 4 : (MAXC <= 4 ? 2 : 1);
-    hipLaunchKernelGGL((moe_decode_down_kernel<HAS_BIAS, MAXC, Q, 2>), dim3(ceil_div(H, 2)), dim3(kDnThreads), 0, s,
-                       glu, w2, b2, idx, route_w, out, T, H, F, E, K);
+    if (one || MAXC > 4) launch_down_k<HAS_BIAS, MAXC, 1, 2>(glu, w2, b2, order, route_w, out, T, H, F, K, s);
+    else launch_down_k<HAS_BIAS, MAXC, (MAXC <= 4 ? 2 : 1), 2>(glu, w2, b2, order, route_w, out, T, H, F, K, s);
 }
 
 // MAXC = 16-byte chunks per lane per row = ceil(len / 512); supported up to 8 (len <= 4096).
@@ -338,12 +391,12 @@ static int pick_maxc(int len) {
 }
 
 #define CMOE_DEC_GU(ACT, BIAS, C) \
-    case C: launch_gateup_t<ACT, BIAS, C>(x, w1, b1, idx, glu, T, H, F, E, K, s); break;
+    case C: launch_gateup_t<ACT, BIAS, C>(x, w1, b1, idx, glu, order, T, H, F, E, K, s); break;
 #define CMOE_DEC_GU_ALL(ACT, BIAS) \
     switch (cg) { CMOE_DEC_GU(ACT, BIAS, 1) CMOE_DEC_GU(ACT, BIAS, 2) CMOE_DEC_GU(ACT, BIAS, 3) \
                   CMOE_DEC_GU(ACT, BIAS, 4) CMOE_DEC_GU(ACT, BIAS, 6) CMOE_DEC_GU(ACT, BIAS, 8) default: break; }
 #define CMOE_DEC_DN(BIAS, C) \
-    case C: launch_down_t<BIAS, C>(glu, w2, b2, idx, route_w, out, T, H, F, E, K, s); break;
+    case C: launch_down_t<BIAS, C>(glu, w2, b2, order, route_w, out, T, H, F, K, s); break;
 #define CMOE_DEC_DN_ALL(BIAS) \
     switch (cd) { CMOE_DEC_DN(BIAS, 1) CMOE_DEC_DN(BIAS, 2) CMOE_DEC_DN(BIAS, 3) CMOE_DEC_DN(BIAS, 4) \
                   CMOE_DEC_DN(BIAS, 6) CMOE_DEC_DN(BIAS, 8) default: break; }
@@ -351,8 +404,8 @@ static int pick_maxc(int len) {
 bool decode_shape_supported(int H, int F) { return pick_maxc(H) > 0 && pick_maxc(F) > 0; }
 
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
-                         const int32_t* idx, const float* route_w, uint16_t* glu, uint16_t* out, int T, int H, int F,
-                         int E, int K, int act, hipStream_t s, hipEvent_t* ev) {
+                         const int32_t* idx, const float* route_w, uint16_t* glu, int32_t* order, uint16_t* out,
+                         int T, int H, int F, int E, int K, int act, hipStream_t s, hipEvent_t* ev) {
     // ev (optional): 3 events recorded before gate_up, after gate_up, after down.
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     if (E > kDecMaxExperts) return hipErrorInvalidValue;
