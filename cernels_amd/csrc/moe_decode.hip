@@ -53,28 +53,61 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int n
     }
 }
 
+// Value of lane l ^ o for o = 1, 2, 8 through DPP (quad_perm, row_ror:8: exact xor partners within a row of 16
+// lanes), else through ds_bpermute.
+template <int O>
+__device__ __forceinline__ float xor_lane(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    if constexpr (O == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false));
+    else if constexpr (O == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false));
+    else if constexpr (O == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false));
+    else return __shfl_xor(v, O, kWave);
+}
+
 // Sum of N per-lane values over the wave, several values per exchange: after the halving steps
 // (offsets 32, 16, ... while more than G values remain), each lane holds G values that are sums over
 // the lanes sharing its upper bits; the remaining single-offset steps complete those G sums in every
 // lane. On return, v[0..G) of lane l hold totals of the value group selected by l's upper bits:
-// group index = lane >> (6 - log2(N/G)).
+// group index = lane >> (6 - log2(N/G)). The completing steps need not pair lane l with l ^ o, only
+// cover the group: offset 4 uses row_half_mirror (l <-> 7 - l within eight lanes), which with the
+// xor-1 and xor-2 steps after it still sums all eight lanes. Lanes of a group may round their totals
+// differently; callers read one fixed lane per group.
+template <int N, int G, int O>
+__device__ __forceinline__ void reduce_step_halving(float (&v)[N], int lane, int n) {
+    const bool upper = lane & O;
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+        if (i >= n / 2) break;
+        const float send = upper ? v[i] : v[i + n / 2];
+        const float keep = upper ? v[i + n / 2] : v[i];
+        v[i] = keep + xor_lane<O>(send);
+    }
+}
+template <int G, int O>
+__device__ __forceinline__ float complete_step(float x) {
+    if constexpr (O == 4)
+        return x + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false));
+    else return x + xor_lane<O>(x);
+}
 template <int N, int G>
 __device__ __forceinline__ void wave_reduce_groups(float (&v)[N], int lane) {
-    int n = N, o = 32;
+    static_assert(N >= G && G >= 1 && (N & (N - 1)) == 0 && (G & (G - 1)) == 0, "powers of two");
+    constexpr int H = N / G;  // halving steps: log2(H), offsets 32, 16, ...
+    static_assert(H <= 8, "halving steps use offsets 32, 16, 8");
+    if constexpr (H >= 2) reduce_step_halving<N, G, 32>(v, lane, N);
+    if constexpr (H >= 4) reduce_step_halving<N, G, 16>(v, lane, N / 2);
+    if constexpr (H >= 8) reduce_step_halving<N, G, 8>(v, lane, N / 4);
 #pragma unroll
-    for (; n > G; n >>= 1, o >>= 1) {
-        const bool upper = lane & o;
-#pragma unroll
-        for (int i = 0; i < n / 2; ++i) {
-            const float send = upper ? v[i] : v[i + n / 2];
-            const float keep = upper ? v[i + n / 2] : v[i];
-            v[i] = keep + __shfl_xor(send, o, kWave);
-        }
+    for (int i = 0; i < G; ++i) {
+        float x = v[i];
+        if constexpr (H < 2) x = complete_step<G, 32>(x);
+        if constexpr (H < 4) x = complete_step<G, 16>(x);
+        if constexpr (H < 8) x = complete_step<G, 8>(x);
+        x = complete_step<G, 4>(x);
+        x = complete_step<G, 2>(x);
+        x = complete_step<G, 1>(x);
+        v[i] = x;
     }
-#pragma unroll
-    for (; o > 0; o >>= 1)
-#pragma unroll
-        for (int i = 0; i < G; ++i) v[i] += __shfl_xor(v[i], o, kWave);
 }
 
 // glu[p, f] = bf16(act(x[t_p] . W1_e[f] + b1_e[f], x[t_p] . W1_e[F+f] + b1_e[F+f])) for the pairs p
@@ -85,7 +118,7 @@ __device__ __forceinline__ void wave_reduce_groups(float (&v)[N], int lane) {
 // on its own (its own LDS bitmap and pair list, ballots, no workgroup barrier), loads the first
 // pair's x row ahead of its weight rows and each further pair's x row while the previous pair is
 // reduced. Measured against one workgroup-wide selection (two barriers, x row loaded per pair):
-// same output bit for bit, 29.9 -> 28.9 us at T=8 (H=1280) and 10.6 -> 10.3 us at T=1 (H=2048).
+// 29.9 -> 28.9 us at T=8 (H=1280) and 10.6 -> 10.3 us at T=1 (H=2048).
 template <int ACT, bool HAS_BIAS, int MAXC, int R>
 __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1, const float* __restrict__ b1,
