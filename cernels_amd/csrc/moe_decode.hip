@@ -158,14 +158,13 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
     for (int c = 0; c < kDecMaxPairs / kWave; ++c)
         if (ev[c] >= 0) atomicOr(&wb[ev[c] >> 5], 1u << (ev[c] & 31));
     uint32_t bw = lane < kDecMaxExperts / 32 ? wb[lane] : 0u;
-    const int cnt = __popc(bw);
-    int incl = cnt;
+    const int cnt = __popc(bw);  // 0..32
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    // exclusive prefix sum of cnt over the lower lanes, bit by bit of cnt (ballots, no LDS round trips)
+    int excl = 0;
 #pragma unroll
-    for (int o = 1; o < kDecMaxExperts / 32; o <<= 1) {
-        const int y = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += y;
-    }
-    const int excl = incl - cnt;
+    for (int b = 0; b < 6; ++b) excl += __popcll(__ballot((cnt >> b) & 1) & lt) << b;
+    const int incl = excl + cnt;
     const bool holder = u >= excl && u < incl;  // at most one lane
     int eh = 0;
     if (holder) {
@@ -177,7 +176,6 @@ __global__ __launch_bounds__(kDecThreads) void moe_decode_gateup_kernel(
     const int e = __builtin_amdgcn_readlane(eh, __ffsll((unsigned long long)hb) - 1);
 
     // ---- pairs of e, ascending p, into this wave's list
-    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
     int np = 0, base = 0;  // base: valid pairs of smaller expert ids (lead wave only)
     if (lead) {
 #pragma unroll
