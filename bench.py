@@ -3,9 +3,10 @@
 
 A step = one call of the experts op (route → gate_up GEMM+SwiGLU → down GEMM+weight → combine,
 or the decode GEMV pair) over one batch of seeded synthetic input already resident in HBM,
-through the C ABI with preallocated output and workspace. The headline is BASELINE.json
-configs[1] (``deepseek_v2_lite_prefill``: T=2048, H=1280, F=896, E=64, top-6); the other
-BASELINE workloads are measured the same way and reported under ``per_config``.
+through the C ABI with preallocated output and workspace. BASELINE.json's metric names no single
+config, so the headline is the largest workload that fits one GPU: ``gpt_oss_20b_experts``
+(T=4096, H=F=2880, E=32, top-4, 815 GFLOP per step). The other BASELINE
+workloads are measured the same way and reported under ``per_config``.
 
 Prefill runs on expert weights packed once in MFMA-fragment order (``cernels_moe_pack_weights``,
 what the drop-in loaders cache on a module at first use); the pack itself is outside the timed
@@ -34,7 +35,10 @@ whichever bounds that kernel at its arithmetic intensity. ``roofline.traffic`` i
 measured HBM bytes per launch: two child runs of this script under ``rocprofv3 --pmc FETCH_SIZE``
 and ``--pmc WRITE_SIZE``, each counter scaled by what it reads for a 256 MiB device copy (started
 before this process touches the GPU; skipped with --no-traffic). ``cpu_baseline`` times the
-op_eager restatement (the reference's baseline) on the host CPU on the same inputs.
+op_eager restatement (the reference's baseline) on the host CPU on the same inputs, for every
+workload that ran (``per_config[...].cpu_baseline``; the headline's is the top-level one).
+``calibration`` times torch's own dense bf16 GEMM (hipBLASLt) on the headline's per-expert shapes
+and on a large square GEMM: what the platform library reaches on this GPU, beside the peak.
 """
 
 from __future__ import annotations
@@ -100,19 +104,23 @@ class Events:
             self.hip.hipEventDestroy(e)
 
 
-def stage_model(shape, U, P, stage):
-    """Algorithmic FLOPs and HBM bytes of one launch of a stage (each distinct expert once)."""
+def stage_model(shape, U, P, stage, path="packed"):
+    """Algorithmic FLOPs and HBM bytes of one launch of a stage (each distinct expert once).
+
+    Y (the down GEMM's per-pair rows, read back by the combine) is fp16 plus one exponent byte per
+    32 columns on the packed path and fp32 on the stored-layout path."""
     T, H, F, E = shape.tokens, shape.hidden, shape.ffn, shape.experts
     if stage == "route":
         return 0.0, P * 4 * 2 + (E + 1) * 8
     if stage == "gate_up":  # weights + fp32 bias, x read, glu bf16 written, pair ids + weights
         w = U * 2 * F * H * 2 + (U * 2 * F * 4 if shape.bias else 0)
         return 2.0 * P * H * 2 * F, w + T * H * 2 + P * F * 2 + P * 8
-    if stage == "down":  # weights + fp32 bias, glu read, fp32 weighted rows written
+    y_bytes = P * H * 2 + P * (H // 32) if path == "packed" else P * H * 4
+    if stage == "down":  # weights + fp32 bias, glu read, weighted rows Y written
         w = U * H * F * 2 + (U * H * 4 if shape.bias else 0)
-        return 2.0 * P * F * H, w + P * F * 2 + P * H * 4 + P * 8
+        return 2.0 * P * F * H, w + P * F * 2 + y_bytes + P * 8
     if stage == "combine":
-        return float(P * H), P * H * 4 + T * H * 2 + P * 4
+        return float(P * H), y_bytes + T * H * 2 + P * 4
     if stage == "decode_gate_up":
         return 2.0 * P * H * 2 * F, U * 2 * F * H * 2 + T * H * 2 + P * F * 2
     if stage == "decode_down":
@@ -312,7 +320,7 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
         mfma_peak_frac=flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS,
         hbm_peak_frac=alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         attainable_frac=t_roof_ms / ms, algorithmic_bytes=alg_bytes, flops=flops,
-        stages={k: dict(ms=v, **roofline_of(*stage_model(shape, U, P, k), v)) for k, v in stage_ms.items()},
+        stages={k: dict(ms=v, **roofline_of(*stage_model(shape, U, P, k, main_path), v)) for k, v in stage_ms.items()},
     )
     if pack_ms is not None:
         rec["pack_ms"] = pack_ms
@@ -378,43 +386,100 @@ def run_module_op(name, steps, warmup, dev, log):
     return rec
 
 
+def cpu_threads():
+    """(threads used, CPUs in this process's affinity mask). The GPU boxes give each GPU a share of the
+    host's cores and say so in OMP_NUM_THREADS; the baseline uses that whole share (or the whole
+    affinity mask where no share is set)."""
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS") or 0)
+    return (min(affinity, share) if share > 0 else affinity), affinity
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(shape, budget_s, log):
-    """Times the op_eager restatement on the host CPU on the headline workload's inputs."""
+    """Times the op_eager restatement (oracle/eager.py, the reference's baseline path) on the host CPU
+    on the workload's own inputs: one warmup run, then runs until ``budget_s`` is spent (at most 5)."""
     import torch
 
     from cernels_amd.configs.synth import make_inputs, make_weights
     from oracle import eager as O
 
-    cores = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(cores)
+    threads, affinity = cpu_threads()
+    torch.set_num_threads(threads)
     inp, wts = make_inputs(shape), make_weights(shape)
-    args = (inp.x, inp.top_k_index, inp.top_k_weights, wts.gate_up_proj, wts.down_proj)
+    args = (inp.x, inp.top_k_index, inp.top_k_weights, wts.gate_up_proj, wts.down_proj, wts.gate_up_proj_bias,
+            wts.down_proj_bias)
+    kw = dict(layout=shape.layout, act=shape.act)
+    t0 = time.perf_counter()
+    O.experts_eager(*args, **kw)  # warmup
+    warm = time.perf_counter() - t0
     times = []
     t_start = time.perf_counter()
-    while True:
+    while len(times) < 5 and (not times or time.perf_counter() - t_start + warm <= budget_s):
         t0 = time.perf_counter()
-        O.experts_eager(*args)
+        O.experts_eager(*args, **kw)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 6:
-            break
-    timed = times[1:] if len(times) > 1 else times
-    med = statistics.median(timed)
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    log(f"[cpu_baseline] {len(times)} runs, median {med * 1e3:.1f} ms on {cores} threads ({cpu})")
-    return dict(
-        value=shape.flops() / med / 1e12, unit="TFLOP/s", cores=torch.get_num_threads(), kind="port",
+    med = statistics.median(times)
+    cpu = _cpu_model()
+    flops = shape.flops()
+    log(f"[cpu_baseline {shape.name}] {len(times)} runs, median {med * 1e3:.2f} ms on {threads} threads "
+        f"({affinity} CPUs in the affinity mask; {cpu})")
+    rec = dict(
+        cores=torch.get_num_threads(), kind="port",
         sample=(f"op_eager restatement (transformers experts forward loop, oracle/eager.py) on the full "
-                f"{shape.name} workload (T={shape.tokens}), bf16 on CPU, {len(times)} runs"
-                f"{' after 1 warmup' if len(times) > 1 else ''}, median {med * 1e3:.1f} ms; CPU: {cpu}"),
-        ms=med * 1e3,
+                f"{shape.name} workload (T={shape.tokens}), bf16 on the host CPU, 1 warmup + {len(times)} timed "
+                f"runs, median {med * 1e3:.2f} ms; {threads} threads = the GPU's share of the host "
+                f"(OMP_NUM_THREADS; {affinity} CPUs in the affinity mask); CPU: {cpu}"),
+        ms=med * 1e3, affinity_cpus=affinity,
     )
+    if shape.decode:
+        U = int(torch.unique(inp.top_k_index).numel())
+        nbytes = U * shape.expert_bytes() + 2 * shape.tokens * shape.hidden * 2 + shape.pairs * 8
+        rec.update(value=nbytes / med / 1e9, unit="GB/s")
+    else:
+        rec.update(value=flops / med / 1e12, unit="TFLOP/s")
+    return rec
+
+
+def dense_gemm_calibration(dev, log, reps=20):
+    """torch's dense bf16 GEMM (hipBLASLt) on this GPU: the headline's per-expert GEMMs at the uniform
+    load (T*k/E = 512 rows per expert) as one batched GEMM over its 32 experts, and an 8192^3 GEMM.
+    Operands are contiguous (row-major A, row-major B)."""
+    import torch
+
+    res = {}
+    shapes = {"gpt_oss_gate_up_bmm_32x512x2880x5760": (32, 512, 2880, 5760),
+              "gpt_oss_down_bmm_32x512x2880x2880": (32, 512, 2880, 2880),
+              "square_8192": (1, 8192, 8192, 8192)}
+    for name, (b, m, k, n) in shapes.items():
+        a = torch.randn(b, m, k, device=dev).bfloat16()
+        w = torch.randn(b, k, n, device=dev).bfloat16()
+        for _ in range(3):
+            torch.bmm(a, w)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            torch.bmm(a, w)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        tf = 2.0 * b * m * k * n / (ms * 1e-3) / 1e12
+        res[name] = dict(ms=round(ms, 5), tflops=round(tf, 1), mfma_peak_frac=round(tf / MFMA_BF16_PEAK_TFS, 4))
+        log(f"[calibration] torch.bmm bf16 {name}: {ms:.4f} ms, {tf:.1f} TFLOP/s ({tf / MFMA_BF16_PEAK_TFS * 100:.1f}% "
+            f"of the {MFMA_BF16_PEAK_TFS:.0f} TFLOP/s peak)")
+        del a, w
+    torch.cuda.empty_cache()
+    return res
 
 
 # ---- HBM traffic per launch (rocprofv3 counters, child processes) ----------------------------------
@@ -486,7 +551,9 @@ def main():
     ap.add_argument("--configs", default="all",
                     help="'all', 'headline', 'module' (only the module-level loader ops) or a comma list of BASELINE "
                          "workload names")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=30.0,
+                    help="CPU-baseline budget over all workloads that ran (split evenly; at least one run each)")
+    ap.add_argument("--no-calibration", action="store_true", help="skip timing torch's dense GEMM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-native", action="store_true", help="skip timing prefill on the weights as stored")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 FETCH/WRITE_SIZE child runs")
@@ -551,10 +618,13 @@ def main():
                     intensity_flop_per_byte=round(dom["intensity"], 2))
     if traffic_mb is None:
         roofline["traffic_note"] = traffic_note or "dominant kernel not in the counter trace"
+    calibration = None if args.no_calibration else dense_gemm_calibration(dev, log)
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(BASELINE_SHAPES[head["workload"]], args.cpu_seconds, log)
-        cpu = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in cpu.items()}
+        for n in names:
+            c = cpu_baseline(BASELINE_SHAPES[n], args.cpu_seconds / len(names), log)
+            per[n]["cpu_baseline"] = {k: (round(v, 6) if isinstance(v, float) else v) for k, v in c.items()}
+        cpu = per[head["workload"]]["cpu_baseline"]
     line = {
         "metric": METRIC,
         "value": round(head["tflops"], 3),
@@ -567,7 +637,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded CPU-generated bf16 x ~ N(0,1), weights ~ N(0,0.02), softmax top-k routing)",
+        "data": "synthetic (seeded CPU-generated bf16 x ~ N(0,1), weights and biases ~ N(0,0.02), seeded router "
+                "logits ~ N(0,1) routed as BASELINE.json states per config)",
         "config": {"workload": head["workload"], "tokens": head["tokens"], "hidden": head["hidden"],
                    "ffn": head["ffn"], "experts": head["experts"], "top_k": head["top_k"],
                    "weights": "packed once (MFMA-fragment order), pack time excluded" if head["path"] == "packed"
@@ -578,15 +649,17 @@ def main():
         "cpu_baseline": cpu,
         "per_config": {
             n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()
-                if k not in ("stages", "native_layout", "router")}
+                if k not in ("stages", "native_layout", "router", "cpu_baseline")}
             | {"stages_ms": {s: round(v["ms"], 5) for s, v in r["stages"].items()}}
             | ({"router": {"ms": round(r["router"]["ms"], 5), "mode": r["router"]["mode"], "bound": r["router"]["bound"],
                            "frac": round(r["router"]["frac"], 4), "torch_ops_ms": round(r["router"]["torch_ms"], 5)}}
                if "router" in r else {})
             | ({"native_layout_ms": round(r["native_layout"]["ms"], 5)} if "native_layout" in r else {})
+            | ({"cpu_baseline": r["cpu_baseline"]} if "cpu_baseline" in r else {})
             for n, r in per.items()
         },
         "module_ops": {n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()} for n, r in mods.items()},
+        "calibration": calibration,
     }
     try:
         Path(args.report).parent.mkdir(parents=True, exist_ok=True)

@@ -3,15 +3,18 @@
 Usage: python -m cernels_amd.modeling.main <model> [--checkpoint DIR] [--layers N] ...
        (<model> = north_mini_code | deepseek_ocr_2, an entry of cernels_amd.modeling.swaps.SWAPS)
 
-Same protocol as the reference's src/modeling/main.py:48-95. For every variant, stock first:
-  - a correctness gate vs stock: greedy-token prefix match over ``--gate-tokens``, and the max abs
-    diff of the last prefill logits (reported, not gated), calibrated by the same two numbers for
-    stock under transformers' other experts implementation (``stock_drift_calibration``);
-  - prefill latency: torch.utils.benchmark median of ``model(**inputs)``;
-  - decode tokens/s: ``decode_tokens / (generate wall - prefill)``, best of ``--runs`` generates.
-The model is the real transformers architecture, from a local checkpoint directory or with seeded
-random weights (cernels_amd.modeling.models), fed seeded random token ids. The result is written
-as JSON (``--out``) and printed.
+The protocol is the reference's (src/modeling/main.py:1-8, :51-76): each variant of the model's
+swap entry, stock first, is
+  - gated against stock by the length of the common prefix of their greedy continuations
+    (``--gate-tokens``) and by the largest difference of their last-position prefill logits
+    (reported, not gated);
+  - timed for prefill (median of repeated forwards of the prompt);
+  - timed for decode (tokens per second of a fixed-length greedy generate, prefill subtracted).
+Two correct bf16 implementations drift apart on a deep model too, so the same two gate numbers are
+also measured between stock and stock under transformers' other experts implementation
+(``stock_drift_calibration``). The model is the real transformers architecture, from a local
+checkpoint directory or with seeded random weights (cernels_amd.modeling.models), fed seeded random
+token ids. The result is written as JSON (``--out``) and printed.
 """
 
 from __future__ import annotations
@@ -19,8 +22,10 @@ from __future__ import annotations
 import argparse
 import json
 import platform
+import statistics
 import sys
 import time
+from dataclasses import dataclass
 from pathlib import Path
 
 import torch
@@ -28,95 +33,116 @@ import torch
 from cernels_amd.modeling import models as M
 from cernels_amd.modeling.swaps import SWAPS
 
-GATE_TOKENS = 64
-DECODE_TOKENS = 128
+
+@dataclass
+class Options:
+    gate_tokens: int = 64     # greedy continuation compared against stock
+    decode_tokens: int = 128  # tokens generated per decode timing run
+    decode_runs: int = 3      # decode timing runs; the fastest is kept
+    prefill_seconds: float = 5.0  # time budget of the prefill repeats
+
+
+@dataclass
+class Trace:
+    """What a model variant answers on the fixed prompt: its greedy continuation and the fp32 logits
+    of the prompt's last position."""
+
+    tokens: torch.Tensor
+    logits: torch.Tensor
+
+    def against(self, ref: "Trace") -> dict:
+        n = int(ref.tokens.numel())
+        differs = (self.tokens[:n] != ref.tokens).nonzero()
+        prefix = int(differs[0, 0]) if differs.numel() else n
+        return {"gate_token_match": f"{prefix}/{n}", "gate_prefix": prefix,
+                "last_logits_max_diff": round(float((self.logits - ref.logits).abs().max()), 4)}
 
 
 def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-@torch.no_grad()
-def greedy(model, inputs, n):
-    out = model.generate(**inputs, max_new_tokens=n, min_new_tokens=n, do_sample=False)
-    return out[0, inputs["input_ids"].size(1):]
+def _generate(model, inputs, n):
+    return model.generate(**inputs, do_sample=False, max_new_tokens=n, min_new_tokens=n)
 
 
-@torch.no_grad()
-def last_logits(model, inputs):
-    return model(**inputs).logits[0, -1].float()
+@torch.inference_mode()
+def trace(model, inputs, n: int) -> Trace:
+    logits = model(**inputs).logits[0, -1].float()
+    seq = _generate(model, inputs, n)
+    return Trace(seq[0, inputs["input_ids"].shape[1]:], logits)
 
 
-@torch.no_grad()
-def time_generate_s(model, inputs, n, runs=3):
-    times = []
-    for _ in range(runs):
+@torch.inference_mode()
+def prefill_seconds(model, inputs, budget_s: float) -> float:
+    """Median wall time of one prompt forward, from HIP events around each repeat, after one warmup,
+    repeated until ``budget_s`` is spent (at least three repeats)."""
+    model(**inputs)
+    times, spent = [], 0.0
+    while len(times) < 3 or spent < budget_s:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        model(**inputs)
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) * 1e-3)
+        spent += times[-1]
+    return statistics.median(times)
+
+
+@torch.inference_mode()
+def decode_rate(model, inputs, n: int, runs: int, prefill_s: float) -> tuple[float, float]:
+    """(tokens per second of the decode part, seconds of the fastest generate): n greedy tokens per
+    generate, the prompt's prefill time taken out."""
+    best = float("inf")
+    for _ in range(max(1, runs)):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        model.generate(**inputs, max_new_tokens=n, min_new_tokens=n, do_sample=False)
+        _generate(model, inputs, n)
         torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-    return min(times)
+        best = min(best, time.perf_counter() - t0)
+    return n / max(best - prefill_s, 1e-9), best
 
 
-@torch.no_grad()
-def prefill_s(model, inputs, min_run_time):
-    from torch.utils.benchmark import Timer
-
-    m = Timer(stmt="model(**inputs)", globals={"model": model, "inputs": inputs}).blocked_autorange(
-        min_run_time=min_run_time)
-    return m.median
-
-
-def run(model, inputs, name, variants=None, gate_tokens=GATE_TOKENS, decode_tokens=DECODE_TOKENS, runs=3,
-        min_run_time=5.0):
-    apply, all_variants = SWAPS[name]
-    variants = list(all_variants if variants is None else variants)
-    if variants[0] != "stock":
-        variants = ["stock"] + [v for v in variants if v != "stock"]
+def sweep(model, inputs, name: str, variants=None, opts: Options | None = None) -> dict:
+    """Measures every variant of SWAPS[name] (stock first) and restores stock at the end."""
+    opts = opts or Options()
+    swap, known = SWAPS[name]
+    order = ["stock"] + [v for v in (known if variants is None else variants) if v != "stock"]
+    ref = None
     results = {}
-    ref_tokens = ref_logits = None
-    for variant in variants:
-        t0 = time.time()
-        apply(model, variant)
-        tokens, logits = greedy(model, inputs, gate_tokens), last_logits(model, inputs)
-        if variant == "stock":
-            ref_tokens, ref_logits = tokens, logits
-        match = int((tokens == ref_tokens).int().cumprod(0).sum())
-        p = prefill_s(model, inputs, min_run_time)
-        gen = time_generate_s(model, inputs, decode_tokens, runs)
-        results[variant] = {
-            "prefill_ms": round(p * 1e3, 2),
-            "decode_tok_s": round(decode_tokens / (gen - p), 2),
-            "generate_s": round(gen, 3),
-            "gate_token_match": f"{match}/{gate_tokens}",
-            "last_logits_max_diff": round((logits - ref_logits).abs().max().item(), 4),
-            "last_logits_std": round(ref_logits.std().item(), 4),
-        }
-        _log(f"{variant}: {results[variant]} ({time.time() - t0:.0f} s)")
-    apply(model, "stock")
+    try:
+        for v in order:
+            t0 = time.time()
+            swap(model, v)
+            tr = trace(model, inputs, opts.gate_tokens)
+            ref = ref or tr
+            p = prefill_seconds(model, inputs, opts.prefill_seconds)
+            rate, gen = decode_rate(model, inputs, opts.decode_tokens, opts.decode_runs, p)
+            results[v] = {"prefill_ms": round(p * 1e3, 2), "decode_tok_s": round(rate, 2), "generate_s": round(gen, 3),
+                          **tr.against(ref), "last_logits_std": round(float(ref.logits.std()), 4)}
+            _log(f"{v}: {results[v]} ({time.time() - t0:.0f} s)")
+    finally:
+        swap(model, "stock")
     return results
 
 
-def stock_drift(model, inputs, gate_tokens=GATE_TOKENS):
-    """The gate's calibration: stock under transformers' other experts implementation (grouped_mm
-    vs eager) against stock as configured. Two correct bf16 implementations drift apart too; on a
-    deep model with random weights they can disagree from the first greedy token."""
+def stock_drift(model, inputs, gate_tokens: int) -> dict:
+    """The gate's calibration: stock under transformers' other experts implementation (grouped_mm vs
+    eager) against stock as configured, by the same two numbers."""
     cfg = getattr(model.config, "text_config", model.config)
     current = cfg._experts_implementation
     other = "eager" if current != "eager" else "grouped_mm"
-    tokens, logits = greedy(model, inputs, gate_tokens), last_logits(model, inputs)
+    base = trace(model, inputs, gate_tokens)
     try:
         model.set_experts_implementation(other)
     except (ValueError, ImportError) as e:  # grouped_mm may not dispatch on this build
         return {"other": other, "error": str(e)}
     try:
-        t2, l2 = greedy(model, inputs, gate_tokens), last_logits(model, inputs)
+        alt = trace(model, inputs, gate_tokens)
     finally:
         model.set_experts_implementation(current)
-    match = int((t2 == tokens).int().cumprod(0).sum())
-    return {"other": other, "gate_token_match": f"{match}/{gate_tokens}",
-            "last_logits_max_diff": round((l2 - logits).abs().max().item(), 4)}
+    return {"other": other, **alt.against(base)}
 
 
 def main(argv=None):
@@ -125,10 +151,11 @@ def main(argv=None):
     ap.add_argument("--checkpoint", help="local transformers checkpoint directory (default: seeded random weights)")
     ap.add_argument("--layers", type=int, help="decoder layers (default: the model's)")
     ap.add_argument("--prefill-tokens", type=int, help="prompt length (default: the reference's)")
-    ap.add_argument("--decode-tokens", type=int, default=DECODE_TOKENS)
-    ap.add_argument("--gate-tokens", type=int, default=GATE_TOKENS)
-    ap.add_argument("--runs", type=int, default=3, help="generate runs per variant (best is kept)")
-    ap.add_argument("--min-run-time", type=float, default=5.0, help="seconds of prefill timing per variant")
+    ap.add_argument("--decode-tokens", type=int, default=Options.decode_tokens)
+    ap.add_argument("--gate-tokens", type=int, default=Options.gate_tokens)
+    ap.add_argument("--runs", type=int, default=Options.decode_runs, help="generate runs per variant (best is kept)")
+    ap.add_argument("--min-run-time", type=float, default=Options.prefill_seconds,
+                    help="seconds of prefill timing per variant")
     ap.add_argument("--variants", help="comma list (stock is always first)")
     ap.add_argument("--stock-experts", choices=["default", "eager", "grouped_mm"], default="default",
                     help="transformers experts implementation of the stock variant")
@@ -151,8 +178,8 @@ def main(argv=None):
          f"{inputs['input_ids'].shape[1]} tokens, decode {args.decode_tokens}; stock experts "
          f"'{cfg._experts_implementation}', attention '{cfg._attn_implementation}'")
     variants = None if not args.variants else [v.strip() for v in args.variants.split(",") if v.strip()]
-    results = run(model, inputs, args.model, variants, args.gate_tokens, args.decode_tokens, args.runs,
-                  args.min_run_time)
+    opts = Options(args.gate_tokens, args.decode_tokens, args.runs, args.min_run_time)
+    results = sweep(model, inputs, args.model, variants, opts)
     drift = stock_drift(model, inputs, args.gate_tokens)
     _log(f"stock drift calibration ({cfg._experts_implementation} vs {drift['other']}): {drift}")
     payload = {

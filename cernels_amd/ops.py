@@ -90,7 +90,9 @@ def moe_experts(
     if out is None:
         out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
     else:
-        _require(out.is_contiguous() and out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H), "bad out tensor")
+        _require(isinstance(out, torch.Tensor) and out.is_cuda and out.device == x.device and out.is_contiguous()
+                 and out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H),
+                 "out must be a contiguous bf16 CUDA tensor [T, H] on x's device")
     if T == 0:
         return out
     with torch.cuda.device(x.device):
@@ -204,15 +206,31 @@ def moe_experts_packed(x: torch.Tensor, packed: PackedExperts, indices: torch.Te
                        topk: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """Routed experts prefill on packed weights (same result contract as moe_experts)."""
     _require(isinstance(packed, PackedExperts), "packed must come from pack_experts")
-    _require(x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2, "x must be bf16 [T, H]")
-    _require(indices.dtype == torch.int32 and indices.is_contiguous(), "indices must be contiguous int32")
-    _require(weights.dtype == torch.float32 and weights.is_contiguous(), "weights must be contiguous float32")
+    _require(isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.bfloat16 and x.is_contiguous()
+             and x.dim() == 2, "x must be a contiguous bf16 CUDA tensor [T, H]")
+    dev = x.device
+    for t, name in ((indices, "indices"), (weights, "weights"), (packed.gate_up, "packed gate_up"),
+                    (packed.down, "packed down"), (packed.gate_up_bias, "gate_up_bias"),
+                    (packed.down_bias, "down_bias")):
+        if t is None and name.endswith("bias"):
+            continue
+        _require(isinstance(t, torch.Tensor) and t.is_cuda and t.device == dev and t.is_contiguous(),
+                 f"{name} must be a contiguous CUDA tensor on x's device ({dev})")
+    _require(indices.dtype == torch.int32, "indices must be int32")
+    _require(weights.dtype == torch.float32, "weights must be float32")
     T, H = map(int, x.shape)
     K = int(topk)
     _require(H == packed.H and tuple(indices.shape) == (T, K) and tuple(weights.shape) == (T, K), "shape mismatch")
+    for b, n in ((packed.gate_up_bias, 2 * packed.F), (packed.down_bias, packed.H)):
+        _require(b is None or (b.dtype == torch.float32 and tuple(b.shape) == (packed.E, n)),
+                 "biases must be float32 [E, 2F] and [E, H]")
     L = _native.lib()
     if out is None:
-        out = torch.empty((T, H), dtype=torch.bfloat16, device=x.device)
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    else:
+        _require(isinstance(out, torch.Tensor) and out.is_cuda and out.device == dev and out.is_contiguous()
+                 and out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H),
+                 "out must be a contiguous bf16 CUDA tensor [T, H] on x's device")
     if T == 0:
         return out
     with torch.cuda.device(x.device):

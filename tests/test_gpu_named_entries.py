@@ -1,0 +1,134 @@
+"""The reference-named C entries, called through ctypes exactly as a torch-op shim would bind them.
+
+These are the library's stand-ins for the reference's torch ops (schemas in
+src/kops/cohere2_moe_experts/torch-ext/torch_binding.cpp:6-13 and
+src/kops/gpt_oss_moe_experts/torch-ext/torch_binding.cpp:7-10):
+``cernels_{cohere2,deepseek_ocr2}_moe_experts[_decode]``, ``cernels_qwen3_next_moe_experts``,
+``cernels_gpt_oss_moe_experts`` and ``cernels_megablocks_moe``. Each takes the expert weights as
+stored, int32 indices and fp32 weights, a workspace and a stream. Every one is run on the golden
+fixture of its model family (transformers' own op_eager output, tests/golden/) and on a
+BASELINE-shaped case, against the fp64 oracle (|out - fp64| <= 2e-2*RMS + half a bf16 ulp) and the
+reference's own allclose(2e-2) against op_eager.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+import torch
+
+from conftest import load_golden
+from helpers import assert_reference_verify, assert_within_tolerance, oracle_eager, oracle_fp64
+from oracle import eager as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN_OF = {
+    "cernels_cohere2_moe_experts": "cohere2_t16",
+    "cernels_cohere2_moe_experts_decode": "cohere2_t1",
+    "cernels_deepseek_ocr2_moe_experts": "deepseek_t12",
+    "cernels_deepseek_ocr2_moe_experts_decode": "deepseek_t12",
+    "cernels_qwen3_next_moe_experts": "qwen3_t10",
+    "cernels_gpt_oss_moe_experts": "gpt_oss_t9",
+}
+BASELINE_OF = {
+    "cernels_cohere2_moe_experts": "a3b_30b_prefill",
+    "cernels_cohere2_moe_experts_decode": "a3b_30b_decode",
+    "cernels_deepseek_ocr2_moe_experts": "deepseek_v2_lite_prefill",
+    "cernels_deepseek_ocr2_moe_experts_decode": "deepseek_v2_lite_decode_t8",
+    "cernels_qwen3_next_moe_experts": "qwen3_next_zipf",
+    "cernels_gpt_oss_moe_experts": "gpt_oss_20b_experts",
+}
+
+
+def _call(entry, c, device, rows=None):
+    """Runs the named entry on case c (CPU tensors) and returns the bf16 output on the CPU."""
+    from cernels_amd import _native
+
+    L = _native.lib()
+    sel = slice(None) if rows is None else rows
+    x = c["x"][sel].contiguous().to(device)
+    idx = c["idx"][sel].to(torch.int32).contiguous().to(device)
+    w = c["w"][sel].float().contiguous().to(device)
+    W1, W2 = c["W1"].contiguous().to(device), c["W2"].contiguous().to(device)
+    T, H = map(int, x.shape)
+    K = int(idx.shape[1])
+    E = int(W1.shape[0])
+    F = int(W1.shape[1] // 2) if c["layout"] == "concat" else int(W1.shape[2] // 2)
+    decode = entry.endswith("_decode")
+    nbytes = (L.cernels_moe_experts_decode_workspace_bytes if decode else L.cernels_moe_experts_workspace_bytes)(
+        T, H, F, E, K)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    fn = getattr(L, entry)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    if entry == "cernels_gpt_oss_moe_experts":
+        b1 = c["b1"].float().contiguous().to(device)
+        b2 = c["b2"].float().contiguous().to(device)
+        st = fn(p(x), p(W1), p(b1), p(W2), p(b2), p(idx), p(w), T, H, F, E, K, p(out), p(ws),
+                ctypes.c_size_t(nbytes), stream)
+    else:
+        st = fn(p(x), p(W1), p(W2), p(idx), p(w), T, H, F, E, K, p(out), p(ws), ctypes.c_size_t(nbytes), stream)
+    _native.check(st, entry)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _golden_case(name):
+    t, meta = load_golden(name)
+    return dict(x=t["x"], idx=t["top_k_index"], w=t["top_k_weights"], W1=t["gate_up_proj"], W2=t["down_proj"],
+                b1=t.get("gate_up_proj_bias"), b2=t.get("down_proj_bias"), layout=meta["layout"], act=meta["act"],
+                eager=t["out"])
+
+
+@pytest.mark.parametrize("entry", sorted(GOLDEN_OF))
+def test_named_entry_on_golden(device, entry):
+    c = _golden_case(GOLDEN_OF[entry])
+    rows = slice(0, 8) if entry.endswith("_decode") else None  # decode takes at most 8 tokens
+    print(f"[named {entry} golden {GOLDEN_OF[entry]}]", flush=True)
+    out = _call(entry, c, device, rows)
+    sel = slice(None) if rows is None else rows
+    assert_reference_verify(out, c["eager"][sel], entry)
+    assert_within_tolerance(out, oracle_fp64(c, sel), entry)
+
+
+@pytest.mark.parametrize("entry", sorted(BASELINE_OF))
+def test_named_entry_on_baseline_shape(device, entry):
+    from cernels_amd.configs.registry import BASELINE_SHAPES
+    from cernels_amd.configs.synth import make_inputs, make_weights
+
+    s = BASELINE_SHAPES[BASELINE_OF[entry]]
+    print(f"[named {entry} on {s.name}] generating", flush=True)
+    inp, wts = make_inputs(s), make_weights(s)
+    c = dict(x=inp.x, idx=inp.top_k_index, w=inp.top_k_weights, W1=wts.gate_up_proj, W2=wts.down_proj,
+             b1=wts.gate_up_proj_bias, b2=wts.down_proj_bias, layout=s.layout, act=s.act)
+    out = _call(entry, c, device)
+    rows = torch.randperm(s.tokens, generator=torch.Generator().manual_seed(0))[:48] if s.tokens > 48 else None
+    o = out if rows is None else out[rows]
+    assert_within_tolerance(o, oracle_fp64(c, rows), entry)
+    assert_reference_verify(o, oracle_eager(c, rows), entry)
+
+
+def test_named_megablocks_entry(device):
+    from cernels_amd import _native
+
+    L = _native.lib()
+    g = torch.Generator().manual_seed(11)
+    T, H, F, E, K, act_id = 300, 256, 192, 8, 2, 0
+    x = torch.randn(T, H, generator=g).bfloat16()
+    w1 = (torch.randn(E, H, F, generator=g) * 0.05).bfloat16()
+    w2 = (torch.randn(E, F, H, generator=g) * 0.05).bfloat16()
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).int()
+    wt = torch.rand(T, K, generator=g)
+    d = [t.contiguous().to(device) for t in (x, w1, w2, idx, wt)]
+    nbytes = L.cernels_megablocks_moe_workspace_bytes(T, H, F, E, K)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=device)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = L.cernels_megablocks_moe(p(d[0]), p(d[1]), p(d[2]), p(d[3]), p(d[4]), T, H, F, E, K, act_id, p(out), p(ws),
+                                  ctypes.c_size_t(nbytes), torch.cuda.current_stream(device).cuda_stream)
+    _native.check(st, "cernels_megablocks_moe")
+    torch.cuda.synchronize()
+    assert_within_tolerance(out.cpu(), O.megablocks_fp64(x, idx, wt, w1, w2, act_id), "cernels_megablocks_moe")

@@ -134,13 +134,54 @@ def test_whole_model_runner_on_a_small_model(device, name, tiny):
     model = M.build(spec, device="cuda", layers=3, **tiny)
     inputs = M.prompt_ids(spec, 40, "cuda", vocab=1000)
     print(f"[whole model {name}]", flush=True)
-    res = runner.run(model, inputs, name, gate_tokens=6, decode_tokens=6, runs=1, min_run_time=0.05)
+    opts = runner.Options(gate_tokens=6, decode_tokens=6, decode_runs=1, prefill_seconds=0.05)
+    res = runner.sweep(model, inputs, name, opts=opts)
     _, variants = swaps.SWAPS[name]
     assert list(res) == list(variants)
-    stock = runner.last_logits(model, inputs)
+    stock = runner.trace(model, inputs, 1).logits
     for v in variants[1:]:
         swaps.SWAPS[name][0](model, v)
-        lv = runner.last_logits(model, inputs)
+        lv = runner.trace(model, inputs, 1).logits
         assert float((lv - stock).abs().max()) <= 0.05 * float(stock.abs().max()) + 1e-3, v
         assert res[v]["decode_tok_s"] > 0
     swaps.SWAPS[name][0](model, "stock")
+
+
+@pytest.mark.gpu
+def test_swapped_model_tracks_fp32_as_closely_as_stock(device):
+    """The whole-model gate with its drift calibration as a check: an 8-layer north_mini_code
+    (Cohere2Moe, real hidden/expert shapes, seeded random weights) run in bf16 three ways — stock
+    grouped_mm, stock eager, swapped to this library (prefill and decode kernels) — is compared with
+    the same model in float32 (eager experts). The swapped model's greedy continuation must agree with
+    the float32 one for at least as many tokens as the worse of transformers' two bf16
+    implementations does, and its last prefill logits must be no further from float32's than 1.25x
+    the further of the two."""
+    import copy
+
+    from cernels_amd.modeling import main as runner
+    from cernels_amd.modeling import models as M
+
+    spec = M.SPECS["north_mini_code"]
+    model = M.build(spec, device="cuda", layers=8, vocab_size=32000)
+    inputs = M.prompt_ids(spec, 300, "cuda", vocab=32000)
+    n = 32
+    print("[fp32 gate] building the float32 copy", flush=True)
+    ref32 = copy.deepcopy(model).float()
+    ref32.set_experts_implementation("eager")
+    ref = runner.trace(ref32, inputs, n)
+    del ref32
+    torch.cuda.empty_cache()
+    got = {}
+    for impl in ("grouped_mm", "eager"):
+        model.set_experts_implementation(impl)
+        got[f"stock_{impl}"] = runner.trace(model, inputs, n).against(ref)
+    model.set_experts_implementation("grouped_mm")
+    swaps.SWAPS["north_mini_code"][0](model, "custom")
+    try:
+        got["custom"] = runner.trace(model, inputs, n).against(ref)
+    finally:
+        swaps.SWAPS["north_mini_code"][0](model, "stock")
+    print(f"[fp32 gate] {got}", flush=True)
+    stock = [got["stock_grouped_mm"], got["stock_eager"]]
+    assert got["custom"]["gate_prefix"] >= min(s["gate_prefix"] for s in stock), got
+    assert got["custom"]["last_logits_max_diff"] <= 1.25 * max(s["last_logits_max_diff"] for s in stock), got
