@@ -107,15 +107,16 @@ class Events:
 def stage_model(shape, U, P, stage, path="packed"):
     """Algorithmic FLOPs and HBM bytes of one launch of a stage (each distinct expert once).
 
-    Y (the down GEMM's per-pair rows, read back by the combine) is fp16 plus one exponent byte per
-    32 columns on the packed path and fp32 on the stored-layout path."""
+    Y (the down GEMM's per-pair rows, read back by the combine) is 24-bit floats (3 bytes) on the packed
+    path and fp32 on the stored-layout path; glu is fp16 (packed) or bf16, 2 bytes either way, plus one
+    exponent byte per 16 glu columns on the packed path."""
     T, H, F, E = shape.tokens, shape.hidden, shape.ffn, shape.experts
     if stage == "route":
         return 0.0, P * 4 * 2 + (E + 1) * 8
     if stage == "gate_up":  # weights + fp32 bias, x read, glu bf16 written, pair ids + weights
         w = U * 2 * F * H * 2 + (U * 2 * F * 4 if shape.bias else 0)
         return 2.0 * P * H * 2 * F, w + T * H * 2 + P * F * 2 + P * 8
-    y_bytes = P * H * 2 + P * (H // 32) if path == "packed" else P * H * 4
+    y_bytes = P * H * 3 if path == "packed" else P * H * 4
     if stage == "down":  # weights + fp32 bias, glu read, weighted rows Y written
         w = U * H * F * 2 + (U * H * 4 if shape.bias else 0)
         return 2.0 * P * F * H, w + P * F * 2 + y_bytes + P * 8
@@ -258,8 +259,8 @@ def run_config(shape, steps, warmup, dev, hip, log, with_native=True):
         ev = Events(hip, 2)
         hip.hipEventRecord(ev.ev[0], ctypes.c_void_p(stream))
         for c in range(copies):
-            p1 = torch.empty_like(W1[c])
-            p2 = torch.empty_like(W2[c])
+            p1 = torch.empty(L.cernels_moe_packed_weight_bytes(H, F, E, _native.GATE_UP), dtype=torch.uint8, device=dev)
+            p2 = torch.empty(L.cernels_moe_packed_weight_bytes(H, F, E, _native.DOWN), dtype=torch.uint8, device=dev)
             _native.check(L.cernels_moe_pack_weights(ptr(W1[c]), H, F, E, layout, _native.GATE_UP, ptr(p1), stream),
                           "pack gate_up")
             _native.check(L.cernels_moe_pack_weights(ptr(W2[c]), H, F, E, layout, _native.DOWN, ptr(p2), stream),

@@ -12,7 +12,7 @@ namespace cmoe {
 struct GemmParams;
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream);
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr);
 size_t route_workspace_bytes(int T, int K, int E);
 int gemm_tile_m();
 int packed_tile_m();
@@ -34,7 +34,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K,
                                  int bias_interleaved, int act, void* out, int32_t* offsets, int32_t* tile_offsets,
                                  int32_t* meta, int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts,
-                                 int max_tiles, uint16_t* glu, float* Y, int8_t* yexp, hipStream_t s, hipEvent_t* ev);
+                                 int max_tiles, uint16_t* glu, float* Y, int8_t* gexp, int8_t* rsig,
+                                 int8_t* psig, hipStream_t s, hipEvent_t* ev);
 hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1, const uint16_t* w2, const float* b2,
                          const int32_t* idx, const float* route_w, uint16_t* glu, int32_t* order, uint16_t* out,
                          int T, int H, int F, int E, int K, int act, hipStream_t s, hipEvent_t* ev);
@@ -49,7 +50,7 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct PrefillWs {
-    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, route_counts, glu, Y, yexp, total;
+    size_t offsets, tile_offsets, meta, sorted_pairs, tile_expert, route_counts, glu, Y, gexp, rsig, psig, total;
     int capacity;
 };
 
@@ -61,13 +62,15 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     size_t o = 0;
     w.offsets = o;      o = align_up(o + sizeof(int32_t) * (E + 1));
     w.tile_offsets = o; o = align_up(o + sizeof(int32_t) * (E + 1));
-    w.meta = o;         o = align_up(o + sizeof(int32_t) * 32);  // [0..1] route totals, [8..23] GEMM work counters
+    w.meta = o;         o = align_up(o + sizeof(int32_t) * 32);  // [0..1] route totals, [8..31] GEMM counters, flags
     w.sorted_pairs = o; o = align_up(o + sizeof(int32_t) * P);
     w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
     w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));
     w.glu = o;          o = align_up(o + sizeof(uint16_t) * P * F);
-    w.Y = o;            o = align_up(o + sizeof(float) * P * H);
-    w.yexp = o;         o = align_up(o + (size_t)P * (H / 32));  // packed path: exponent per 32-column Y segment
+    w.Y = o;            o = align_up(o + sizeof(float) * P * H);  // fp32 (stored layout) or 24-bit floats (packed)
+    w.gexp = o;         o = align_up(o + (size_t)P * (F / 16));  // packed path: exponent per 16-column glu segment
+    w.rsig = o;         o = align_up(o + (size_t)P);             // packed path: per glu row scale
+    w.psig = o;         o = align_up(o + (size_t)P);             // packed path: the same, per pair
     w.total = o;
     return w;
 }
@@ -249,7 +252,8 @@ int cernels_moe_experts_packed_staged(const void* x, const void* gate_up_packed,
         reinterpret_cast<int32_t*>(base + w.tile_offsets), reinterpret_cast<int32_t*>(base + w.meta),
         reinterpret_cast<int32_t*>(base + w.sorted_pairs), reinterpret_cast<int32_t*>(base + w.tile_expert),
         reinterpret_cast<int32_t*>(base + w.route_counts), w.capacity, reinterpret_cast<uint16_t*>(base + w.glu),
-        reinterpret_cast<float*>(base + w.Y), reinterpret_cast<int8_t*>(base + w.yexp), stream, stage_events));
+        reinterpret_cast<float*>(base + w.Y), reinterpret_cast<int8_t*>(base + w.gexp), reinterpret_cast<int8_t*>(base + w.rsig),
+        reinterpret_cast<int8_t*>(base + w.psig), stream, stage_events));
 }
 
 int cernels_moe_experts_packed(const void* x, const void* gate_up_packed, const float* gate_up_bias,

@@ -85,6 +85,39 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return (uint32_t)f32_to_bf16_bits(a) | ((uint32_t)f32_to_bf16_bits(b) << 16);
 }
 
+// Two fp32 values -> two round-to-nearest-even fp16 in one dword (low half = a).
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
+// 24-bit floats: the top 24 bits of the fp32 pattern (sign, 8-bit exponent, 15-bit mantissa), rounded
+// to nearest even on the 8 dropped bits (2^-16 relative rounding, fp32's range). inf stays inf and
+// nan stays nan. Four of them pack into three dwords, value i in bytes 3i..3i+2.
+__device__ __forceinline__ uint32_t f32_to_f24(float f) {
+    const uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (u >> 8) | ((u & 0xffu) ? 1u : 0u);
+    return (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
+}
+__device__ __forceinline__ float f24_to_f32(uint32_t r) { return __uint_as_float(r << 8); }
+struct f24x4 {
+    uint32_t d[3];
+};
+__device__ __forceinline__ f24x4 pack_f24x4(float a, float b, float c, float e) {
+    const uint32_t r0 = f32_to_f24(a), r1 = f32_to_f24(b), r2 = f32_to_f24(c), r3 = f32_to_f24(e);
+    return f24x4{{r0 | (r1 << 24), (r1 >> 8) | (r2 << 16), (r2 >> 16) | (r3 << 8)}};
+}
+__device__ __forceinline__ f32x4 unpack_f24x4(const f24x4& p) {
+    return f32x4{f24_to_f32(p.d[0] & 0xffffffu), f24_to_f32((p.d[0] >> 24) | ((p.d[1] & 0xffffu) << 8)),
+                 f24_to_f32((p.d[1] >> 16) | ((p.d[2] & 0xffu) << 16)), f24_to_f32(p.d[2] >> 8)};
+}
+
+// Full-wave (64-lane) maximum; every lane returns it.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
 // Full-wave (64-lane) sum; every lane returns the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

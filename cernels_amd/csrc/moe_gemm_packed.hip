@@ -2,7 +2,8 @@
 //
 // Same mathematics as the grouped GEMMs on the transformers layouts (moe_gemm.hip):
 //   GEMM1  glu[r, :] = act( X[tok(r), :] · W1_e + b1_e )        SwiGLU / gpt-oss gate in the epilogue
-//   GEMM2  Y[p, :]   = w_p · ( glu[r, :] · W2_e + b2_e )        routing weight in the epilogue (fp32)
+//   GEMM2  Y[p, :]   = w_p · ( glu[r, :] · W2_e )                routing weight in the epilogue (fp32)
+//   combine out[t, :] = sum_k Y[t*K + k, :] + w_p · b2_e            down bias with the k-sum
 // and the same route kernel, item list and deterministic k-sum combine. What changes is how the
 // weights reach the matrix cores. The weights are re-laid once (cernels_moe_pack_weights) so that
 // each 32x16 MFMA operand fragment is 1 KB of contiguous memory in exactly the order a wave's lanes
@@ -22,6 +23,17 @@
 //
 // GEMM1 fragments hold 16 gate and the 16 matching up columns, so one wave holds both inputs of the
 // gated activation for its 16 glu columns; a v_permlane16_swap pairs them up in the epilogue.
+//
+// Precision of the second projection. glu (the activation output, GEMM2's A operand) is stored as
+// fp16, not bf16: 2^-11 relative rounding instead of 2^-8, which is what keeps the output within
+// 2e-2*RMS of the exact value (a bf16 glu alone costs up to ~0.008*RMS). The down weights are packed
+// as fp16 too (MFMA operands share one type), each 32-column fragment scaled by a power of two so its
+// largest |w| sits in [2^14, 2^15): the conversion from bf16 is exact there, and the epilogue
+// multiplies the fragment's columns back by that power of two. A glu segment (a row's 16 or 32
+// columns of one GEMM1 wave) whose largest |glu| reaches 2^15 is stored scaled by 2^-s (s >= 1, so it
+// cannot overflow fp16) and its row is marked; a small kernel between the two GEMMs then brings every
+// marked row to one scale and records it, which GEMM2 folds into the row's routing weight. Without
+// such rows (the normal case) that kernel reads one flag and exits.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -38,6 +50,8 @@ constexpr int kPkABytes = kPkBM * kBK * 2;  // 32 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
 constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
 constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kModePkGateUp = 0;
 constexpr int kModePkDown = 1;
@@ -60,9 +74,12 @@ __host__ __device__ inline long long packed_frag(int e, int c, int ks, int NF, i
 
 // ---- packing (one-time, per weight tensor) ---------------------------------------------------------
 // One thread per 16-byte lane chunk of the packed output, in logical (e, c, ks, lane) order.
+// WHICH 0: gate_up (bf16). WHICH 1: down or the non-gated first projection. For down, `exps` holds
+// the per-(expert, fragment) power of two of each 32-column fragment and the chunk is converted to
+// fp16 scaled by it; for the non-gated first projection `exps` is null and the chunk stays bf16.
 template <int WHICH, int LAYOUT>
 __global__ __launch_bounds__(256) void moe_pack_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                                       int E, int H, int F) {
+                                                       int E, int H, int F, const int8_t* __restrict__ exps) {
     const int Kd = WHICH == 0 ? H : F;
     const int NF = WHICH == 0 ? F / 16 : H / 32;
     const int KS = Kd / 16;
@@ -101,28 +118,80 @@ __global__ __launch_bounds__(256) void moe_pack_kernel(const uint16_t* __restric
             v = u32x4{t[0] | (uint32_t)t[1] << 16, t[2] | (uint32_t)t[3] << 16, t[4] | (uint32_t)t[5] << 16,
                       t[6] | (uint32_t)t[7] << 16};
         }
+        if (exps) {  // bf16 -> fp16 * 2^-s: exact while the scaled value is a normal fp16
+            const int sc = -(int)exps[(long long)e * NF + c];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = pack_f16x2(__builtin_amdgcn_ldexpf(bf16_lo(v[j]), sc),
+                                                          __builtin_amdgcn_ldexpf(bf16_hi(v[j]), sc));
+        }
     }
     *reinterpret_cast<u32x4*>(dst + packed_frag(e, c, ks, NF, KS) * kPkFrag + lane * 8) = v;
 }
 
+// Power of two of each 32-column fragment of a down projection: s with max|w| * 2^-s in [2^14, 2^15)
+// (0 for an all-zero fragment). One workgroup per (expert, fragment); the fragment is 32 output rows of
+// [E, H, F] (contiguous) or 32 output columns of [E, F, H].
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void moe_pack_exp_kernel(const uint16_t* __restrict__ src, int8_t* __restrict__ exps,
+                                                           int H, int F) {
+    const int NF = H / 32;
+    const int e = blockIdx.x / NF, c = blockIdx.x - e * NF;
+    float m = 0.f;
+    if constexpr (LAYOUT == kLayoutConcat) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(src + ((long long)e * H + 32 * c) * F);
+        for (int i = threadIdx.x; i < 32 * F / 8; i += blockDim.x) {
+            const u32x4 v = p[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf16_lo(v[j])), fabsf(bf16_hi(v[j]))));
+        }
+    } else {
+        for (int i = threadIdx.x; i < F * 4; i += blockDim.x) {  // row k, 16-byte chunk i % 4 of the 32 columns
+            const u32x4 v = *reinterpret_cast<const u32x4*>(src + ((long long)e * F + i / 4) * H + 32 * c + 8 * (i % 4));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, fmaxf(fabsf(bf16_lo(v[j])), fabsf(bf16_hi(v[j]))));
+        }
+    }
+    m = wave_max(m);
+    __shared__ float part[4];
+    if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float mm = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+        exps[blockIdx.x] = (int8_t)(mm > 0.f ? max(-100, min(100, __builtin_amdgcn_frexp_expf(mm) - 15)) : 0);
+    }
+}
+
+// Bytes of the per-(expert, fragment) exponent table that follows the packed down weights.
+static size_t down_exp_bytes(int H, int E) { return ((size_t)E * (H / 32) + 255) / 256 * 256; }
+
 size_t packed_weight_bytes(int H, int F, int E, int which) {
-    // every projection keeps its element count: 2FH (gate_up), HF (down, up)
-    return which == 0 ? (size_t)E * 2 * F * H * 2 : (size_t)E * H * F * 2;
+    // gate_up: 2FH bf16; down: HF fp16 + the exponent table; non-gated first projection: HF bf16
+    if (which == 0) return (size_t)E * 2 * F * H * 2;
+    return (size_t)E * H * F * 2 + (which == 1 ? down_exp_bytes(H, E) : 0);
 }
 
 hipError_t launch_pack(const uint16_t* src, uint16_t* dst, int E, int H, int F, int layout, int which, hipStream_t s) {
-    // up ([E, F, H] concat = rows are outputs, or [E, H, F] interleaved = k-major) is a down
-    // projection with H and F exchanged
-    if (which == 2) return launch_pack(src, dst, E, F, H, layout, 1, s);
-    const long long chunks = (long long)E * (which == 0 ? 2LL * F * H : (long long)H * F) / 8;  // = E*NF*KS*64
-    const unsigned grid = (unsigned)((chunks + 255) / 256);
     if (which == 0) {
-        if (layout == kLayoutConcat) hipLaunchKernelGGL((moe_pack_kernel<0, kLayoutConcat>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F);
-        else hipLaunchKernelGGL((moe_pack_kernel<0, kLayoutInterleaved>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F);
-    } else {
-        if (layout == kLayoutConcat) hipLaunchKernelGGL((moe_pack_kernel<1, kLayoutConcat>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F);
-        else hipLaunchKernelGGL((moe_pack_kernel<1, kLayoutInterleaved>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F);
+        const long long chunks = (long long)E * 2LL * F * H / 8;  // = E*NF*KS*64
+        const unsigned grid = (unsigned)((chunks + 255) / 256);
+        if (layout == kLayoutConcat) hipLaunchKernelGGL((moe_pack_kernel<0, kLayoutConcat>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F, nullptr);
+        else hipLaunchKernelGGL((moe_pack_kernel<0, kLayoutInterleaved>), dim3(grid), dim3(256), 0, s, src, dst, E, H, F, nullptr);
+        return hipGetLastError();
     }
+    // up ([E, F, H] concat = rows are outputs, or [E, H, F] interleaved = k-major) is a down projection
+    // with H and F exchanged, kept in bf16 (its A operand is x)
+    const int Hd = which == 2 ? F : H, Fd = which == 2 ? H : F;
+    int8_t* exps = nullptr;
+    if (which == 1) {
+        exps = reinterpret_cast<int8_t*>(dst + (long long)E * H * F);
+        const unsigned g = (unsigned)(E * (H / 32));
+        if (layout == kLayoutConcat) hipLaunchKernelGGL((moe_pack_exp_kernel<kLayoutConcat>), dim3(g), dim3(256), 0, s, src, exps, H, F);
+        else hipLaunchKernelGGL((moe_pack_exp_kernel<kLayoutInterleaved>), dim3(g), dim3(256), 0, s, src, exps, H, F);
+    }
+    const long long chunks = (long long)E * Hd * Fd / 8;
+    const unsigned grid = (unsigned)((chunks + 255) / 256);
+    if (layout == kLayoutConcat) hipLaunchKernelGGL((moe_pack_kernel<1, kLayoutConcat>), dim3(grid), dim3(256), 0, s, src, dst, E, Hd, Fd, exps);
+    else hipLaunchKernelGGL((moe_pack_kernel<1, kLayoutInterleaved>), dim3(grid), dim3(256), 0, s, src, dst, E, Hd, Fd, exps);
     return hipGetLastError();
 }
 
@@ -138,14 +207,18 @@ struct PkParams {
     const int32_t* tile_expert;    // [tiles]
     const int32_t* meta;           // [0] = M-tiles
     const float* route_w;          // [P] (GEMM2)
-    void* out;                     // GEMM1: glu bf16 [P, F]; GEMM2: Y fp32 [P, H]
+    void* out;                     // GEMM1: glu fp16 [P, F]; GEMM2: Y as 24-bit floats [P, H]
     int Kd, NF, KS, n_tiles;
     int F, H, topk;
     int bias_interleaved;          // GEMM1 bias order: 0 = [gate F | up F], 1 = gate/up interleaved
     int a_bytes;                   // GEMM1: bytes of x (< 2^31, checked by the caller)
     int fw;                        // fragments per item (<= kPkWaves); waves past fw idle
     int* counters;                 // [8] per-XCD work counters, zeroed by the route kernel
-    int8_t* yexp;                  // GEMM2: [P, H/32] exponent of each 32-column row segment of Y
+    int8_t* gexp;                  // GEMM1: [F/16, p_cap] exponent of each 16-column glu row segment
+    int8_t* rsig;                  // [P] per glu row: 0, or (GEMM1) 1 = has a scaled segment, then its scale
+    int32_t* sync;                 // [2]: [1] = "some glu segment is scaled"; zeroed by the route kernel
+    int p_cap;                     // row stride of gexp (T*K)
+    const int8_t* wexp;            // GEMM2: [E, NF] power of two of each packed fp16 weight fragment
 };
 
 
@@ -160,6 +233,9 @@ template <int MODE, int ACT, bool HAS_BIAS, bool XPF, bool ODD>
 __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams prm) {
     static_assert(XPF || ODD, "a single-stage reduction is odd");
     static_assert(MODE != kModePkUp || !HAS_BIAS, "the non-gated projection has no bias");
+    static_assert(MODE != kModePkDown || !HAS_BIAS, "the down bias is added by the combine");
+    // GEMM2 multiplies fp16 glu by fp16 weights; the first projections bf16 x by bf16 weights.
+    using OpT = std::conditional_t<MODE == kModePkDown, f16x8, bf16x8>;
     // the first projection gathers token rows of x through the pair list; down reads its own glu rows
     constexpr bool kGather = MODE != kModePkDown;
     __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kPkABytes];
@@ -168,6 +244,9 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     __shared__ int s_pair[2][kPkBM];
     __shared__ float s_w[2][kPkBM];
     __shared__ __attribute__((aligned(16))) float s_bias[2][2 * kPkGlu];
+    // GEMM2: power of two of each wave's weight fragment (entry t holds fragment t % 8: every table
+    // thread stores one, which keeps the table store free of a branch of its own)
+    __shared__ int s_wx[2][kPkBM];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
@@ -237,11 +316,16 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
             return prm.bias[(long long)w.e * prm.H + col];
         }
     };
-    auto tab_store = [&](int buf, int pair, float w, float bias) {
+    // GEMM2: the power of two of wave t's weight fragment.
+    auto tab_wexp = [&](const WorkItem& w) {
+        return (int)prm.wexp[(long long)w.e * prm.NF + min(w.n_idx * prm.fw + (tid & (kPkWaves - 1)), prm.NF - 1)];
+    };
+    auto tab_store = [&](int buf, int pair, float w, float bias, int wx) {
         if (tid < kPkBM) {
             if constexpr (MODE == kModePkDown) {
                 s_pair[buf][tid] = pair;
                 s_w[buf][tid] = w;
+                s_wx[buf][tid] = wx;
             }
             if constexpr (HAS_BIAS) s_bias[buf][tid] = bias;
         }
@@ -283,9 +367,12 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
             if constexpr (kGather) pr[i] = prm.sorted_pairs[a_row(w, i)];
             else pr[i] = a_row(w, i);
         }
-        int pair = 0;
+        int pair = 0, wx = 0;
         float rw = 0.f, bias = 0.f;
-        if constexpr (MODE == kModePkDown) pair = tab_pair(w);
+        if constexpr (MODE == kModePkDown) {
+            pair = tab_pair(w);
+            wx = tab_wexp(w);
+        }
         if constexpr (HAS_BIAS) bias = tab_bias(w);
 #pragma unroll
         for (int i = 0; i < kPkMB / 2; ++i)
@@ -297,7 +384,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         for (int q = 0; q < 4; ++q) breg[0][q] = b_ld(rb_cur, bstep_cur, 0, q);
 #pragma unroll
         for (int q = 0; q < 4; ++q) breg[1][q] = b_ld(rb_cur, bstep_cur, min(1, nst - 1), q);
-        tab_store(tb, pair, rw, bias);
+        tab_store(tb, pair, rw, bias, wx);
         __syncthreads();  // without prefetch the previous item's only step may still read buffer 0
         store_a(IC<kPkMB / 2>{}, IC<0>{});
     };
@@ -334,7 +421,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
             // its rows (all four chunks; rows past the item's blocks are never read).
             constexpr int NA = NMB > 0 ? (NMB + 1) / 2 : kPkMB / 2;
             int nxr[kPkMB / 2];                       // next item's rows (GEMM1: pair ids), KIND 1 -> 2
-            int npair = 0;
+            int npair = 0, nwx = 0;
             float nbias = 0.f;
             // KIND 0: ordinary step; 1: second to last (next item's weight stage 0, rows, tables);
             // 2: last (next item's activation stage 0, all 256 rows, and weight stage 1).
@@ -344,7 +431,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 __syncthreads();  // stage s is in LDS buffer b; every wave is done with the other buffer
                 const unsigned char* sA = smem + b * kPkABytes;
                 auto read_af = [&](int q, int mb) {
-                    return *reinterpret_cast<const bf16x8*>(sA + lds_off(mb * 32 + (lane & 31), 2 * q + (lane >> 5)));
+                    return *reinterpret_cast<const OpT*>(sA + lds_off(mb * 32 + (lane & 31), 2 * q + (lane >> 5)));
                 };
                 float nw = 0.f;
                 if constexpr (KIND == 2) {
@@ -354,7 +441,10 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                             a_cur[i] = a_off(nx, kGather ? nxr[i] / prm.topk : nxr[i]);
 #pragma unroll
                         for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_nx, a_cur[i], 0);
-                        if constexpr (MODE == kModePkDown) nw = prm.route_w[npair];
+                        if constexpr (MODE == kModePkDown) {
+                            nw = prm.route_w[npair];
+                            nwx = tab_wexp(nx);
+                        }
                     }
                 } else {
 #pragma unroll
@@ -373,7 +463,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 // slot k % R, which is then refilled with fragment k + R, R MFMAs ahead of its use.
                 constexpr int R = NMB < 4 ? (NMB > 0 ? NMB : 1) : 4;
                 constexpr int NK = 4 * NMB;
-                bf16x8 af[R];
+                OpT af[R];
                 if constexpr (NMB > 0) {
 #pragma unroll
                 for (int k = 0; k < R; ++k) af[k] = read_af(k / NMB, k % NMB);
@@ -385,13 +475,16 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     __builtin_amdgcn_sched_barrier(0);
                     __builtin_amdgcn_s_setprio(1);
                     __builtin_amdgcn_sched_barrier(0);
-                    const bf16x8 bq = __builtin_bit_cast(bf16x8, breg[b][q]);
+                    const OpT bq = __builtin_bit_cast(OpT, breg[b][q]);
 #pragma unroll
                     for (int mb = 0; mb < NMB; ++mb) {
                         const int k = q * NMB + mb;
                         // Weights as the first operand: the accumulator comes out transposed, each lane
                         // holding four consecutive output columns of one row.
-                        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq, af[k % R], acc[mb], 0, 0, 0);
+                        if constexpr (MODE == kModePkDown)
+                            acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bq, af[k % R], acc[mb], 0, 0, 0);
+                        else
+                            acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq, af[k % R], acc[mb], 0, 0, 0);
                         if (k + R < NK) af[k % R] = read_af((k + R) / NMB, (k + R) % NMB);
                     }
                     if constexpr (KIND == 0) breg[b][q] = b_ld(rb_cur, bstep_cur, s + 2, q);
@@ -417,7 +510,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 if constexpr (KIND == 2) {
                     if constexpr (XPF) {
                         store_a(IC<kPkMB / 2>{}, IC<1 - b>{});
-                        tab_store(tb ^ 1, npair, nw, nbias);
+                        tab_store(tb ^ 1, npair, nw, nbias, nwx);
                     }
                 } else {
                     store_a(IC<NA>{}, IC<1 - b>{});
@@ -469,96 +562,140 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         // stores here: a global load would have to wait for the next item's weights in flight.
         if (active) {
             const int c4 = 4 * (lane >> 5);
+            // glu stores: fp16 segments (16 columns per lane pair for gate_up, 32 for the non-gated
+            // projection), each with its power of two s in gexp: 0, unless some |glu| of the segment is
+            // 2^15 or more (or not finite); then the segment is stored again, scaled by 2^-s.
+            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+            auto glu_scale = [](float m) {  // s >= 1 with m * 2^-s < 2^15 (m >= 2^15, or inf: s = 1)
+                return max(1, __builtin_amdgcn_frexp_expf(m) - 15);
+            };
+            auto mark_scaled = [&](long long r) {
+                if (lane < 32) prm.rsig[r] = 1;
+                prm.sync[1] = 1;
+            };
             if constexpr (MODE == kModePkGateUp) {
                 // Fragment columns 0-15 are gate, 16-31 the matching up columns: elements r (< 8) and
                 // r + 8 of one lane are gate and up of the same glu column.
-                uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+                auto glu4 = [&](int mb, int i, float* v) {
+                    f32x4 g4 = {0.f, 0.f, 0.f, 0.f}, u4 = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (HAS_BIAS) {
+                        g4 = *reinterpret_cast<const f32x4*>(&s_bias[tb][16 * wave + 8 * i + c4]);
+                        u4 = *reinterpret_cast<const f32x4*>(&s_bias[tb][kPkGlu + 16 * wave + 8 * i + c4]);
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        float gv = acc[mb][4 * i + jj], uv = acc[mb][8 + 4 * i + jj];
+                        if constexpr (HAS_BIAS) {  // x + 0.f is not folded (signed zero): add only a real bias
+                            gv += g4[jj];
+                            uv += u4[jj];
+                        }
+                        v[jj] = swiglu<ACT>(gv, uv);
+                    }
+                };
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
                     const int row = mb * 32 + (lane & 31);
-                    if (row < rows) {
+                    if (row < rows) {  // lanes l and l ^ 32 hold the same row
+                        const long long r = row_begin + row;
+                        uint16_t* g = glu + r * prm.F + 16 * fc + c4;
+                        bool big = false;
 #pragma unroll
                         for (int i = 0; i < 2; ++i) {
-                            f32x4 g4 = {0.f, 0.f, 0.f, 0.f}, u4 = {0.f, 0.f, 0.f, 0.f};
-                            if constexpr (HAS_BIAS) {
-                                g4 = *reinterpret_cast<const f32x4*>(&s_bias[tb][16 * wave + 8 * i + c4]);
-                                u4 = *reinterpret_cast<const f32x4*>(&s_bias[tb][kPkGlu + 16 * wave + 8 * i + c4]);
-                            }
                             float v[4];
+                            glu4(mb, i, v);
+                            big |= !(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) < 32768.f);
+                            *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+                        }
+                        if (lane < 32) prm.gexp[(long long)fc * prm.p_cap + r] = 0;
+                        if (__shfl_xor((int)big, 32, kWave) | (int)big) {  // rare: store the segment scaled
+                            float v[2][4];
+                            float m = 0.f;
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj) {
-                                float gv = acc[mb][4 * i + jj], uv = acc[mb][8 + 4 * i + jj];
-                                if constexpr (HAS_BIAS) {  // x + 0.f is not folded (signed zero): add only a real bias
-                                    gv += g4[jj];
-                                    uv += u4[jj];
-                                }
-                                v[jj] = swiglu<ACT>(gv, uv);
+                            for (int i = 0; i < 2; ++i) {
+                                glu4(mb, i, v[i]);
+#pragma unroll
+                                for (int jj = 0; jj < 4; ++jj) m = fmaxf(m, fabsf(v[i][jj]));
                             }
-                            *reinterpret_cast<u32x2*>(glu + (long long)(row_begin + row) * prm.F + 16 * fc + 8 * i + c4) =
-                                u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                            const int sg = glu_scale(fmaxf(m, __shfl_xor(m, 32, kWave)));
+#pragma unroll
+                            for (int i = 0; i < 2; ++i)
+                                *reinterpret_cast<u32x2*>(g + 8 * i) =
+                                    u32x2{pack_f16x2(__builtin_amdgcn_ldexpf(v[i][0], -sg), __builtin_amdgcn_ldexpf(v[i][1], -sg)),
+                                          pack_f16x2(__builtin_amdgcn_ldexpf(v[i][2], -sg), __builtin_amdgcn_ldexpf(v[i][3], -sg))};
+                            if (lane < 32) prm.gexp[(long long)fc * prm.p_cap + r] = (int8_t)sg;
+                            mark_scaled(r);
                         }
                     }
                 }
             } else if constexpr (MODE == kModePkUp) {
-                // 16 columns of the fragment per lane (8i + c4 + jj), activation, bf16 glu row.
-                uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
+                // 16 columns of the fragment per lane (8i + c4 + jj), activation, fp16 glu row segment of
+                // 32 columns (two gexp entries).
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
                     const int row = mb * 32 + (lane & 31);
-                    if (row < rows) {
+                    if (row < rows) {  // lanes l and l ^ 32 hold the same row
+                        const long long r = row_begin + row;
+                        uint16_t* g = glu + r * prm.F + 32 * fc + c4;
+                        bool big = false;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             float v[4];
 #pragma unroll
                             for (int jj = 0; jj < 4; ++jj) v[jj] = act_plain<ACT>(acc[mb][4 * i + jj]);
-                            *reinterpret_cast<u32x2*>(glu + (long long)(row_begin + row) * prm.F + 32 * fc + 8 * i + c4) =
-                                u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                            big |= !(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) < 32768.f);
+                            *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+                        }
+                        if (lane < 32) {
+                            prm.gexp[(long long)(2 * fc) * prm.p_cap + r] = 0;
+                            prm.gexp[(long long)(2 * fc + 1) * prm.p_cap + r] = 0;
+                        }
+                        if (__shfl_xor((int)big, 32, kWave) | (int)big) {  // rare: store the segment scaled
+                            float m = 0.f;
+#pragma unroll
+                            for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(act_plain<ACT>(acc[mb][q])));
+                            const int sg = glu_scale(fmaxf(m, __shfl_xor(m, 32, kWave)));
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                float v[4];
+#pragma unroll
+                                for (int jj = 0; jj < 4; ++jj)
+                                    v[jj] = __builtin_amdgcn_ldexpf(act_plain<ACT>(acc[mb][4 * i + jj]), -sg);
+                                *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+                            }
+                            if (lane < 32) {
+                                prm.gexp[(long long)(2 * fc) * prm.p_cap + r] = (int8_t)sg;
+                                prm.gexp[(long long)(2 * fc + 1) * prm.p_cap + r] = (int8_t)sg;
+                            }
+                            mark_scaled(r);
                         }
                     }
                 }
             } else {
-                // Y row segments of 32 columns (this wave's fragment) in fp16 with a shared power-of-two
-                // exponent k: Y = fp16(y * 2^-k) * 2^k, k chosen so the segment's largest |y| scales
-                // below 2^14 (no fp16 overflow; rounding 2^-11 relative, vs 2^-8 for bf16). A row's two
-                // 16-column halves sit in lanes l and l ^ 32.
-                uint16_t* Yh = reinterpret_cast<uint16_t*>(prm.out);
-                const int NFH = prm.H / 32;
+                // Y rows as 24-bit floats (fp32 rounded to 16 mantissa bits, 2^-16 relative), four
+                // consecutive columns per 12-byte store: the combine sums the K rows of a token from
+                // nearly exact values, at 3/4 of fp32's bytes.
+                unsigned char* Yb = reinterpret_cast<unsigned char*>(prm.out);
+                const float wsc = __builtin_amdgcn_ldexpf(1.0f, s_wx[tb][wave]);  // the fragment's fp16 scale
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
                     const int row = mb * 32 + (lane & 31);
-                    const int rc = min(row, kPkBM - 1);
-                    const float w = s_w[tb][rc];
-                    float a[16];
-                    float m = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        f32x4 bn = {0.f, 0.f, 0.f, 0.f};
-                        if constexpr (HAS_BIAS) bn = *reinterpret_cast<const f32x4*>(&s_bias[tb][32 * wave + 8 * i + c4]);
-#pragma unroll
-                        for (int jj = 0; jj < 4; ++jj) {
-                            float v = acc[mb][4 * i + jj];
-                            if constexpr (HAS_BIAS) v += bn[jj];
-                            a[4 * i + jj] = v * w;
-                            m = fmaxf(m, fabsf(a[4 * i + jj]));
-                        }
-                    }
-                    m = fmaxf(m, __shfl_xor(m, 32, kWave));
-                    const int k = max(-128, min(127, __builtin_amdgcn_frexp_expf(m) - 14));
                     if (row < rows) {
+                        const float w = s_w[tb][row];
                         const long long p = s_pair[tb][row];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            uint32_t hb[4];
+                            float a[4];
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj)
-                                hb[jj] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(a[4 * i + jj], -k));
-                            *reinterpret_cast<u32x2*>(Yh + p * prm.H + 32 * fc + 8 * i + c4) =
-                                u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+                            for (int jj = 0; jj < 4; ++jj) {
+                                const float v = acc[mb][4 * i + jj] * wsc;
+                                a[jj] = v * w;
+                            }
+                            const f24x4 q = pack_f24x4(a[0], a[1], a[2], a[3]);
+                            __builtin_memcpy(Yb + (p * prm.H + 32 * fc + 8 * i + c4) * 3, &q, 12);
                         }
-                        if (lane < 32) prm.yexp[p * NFH + fc] = (int8_t)k;
                     }
                 }
             }
@@ -610,31 +747,78 @@ static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s)
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream);
-// out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] ), slots in k order, Y in the
-// fp16-with-segment-exponent form the packed down GEMM writes. One workgroup per token; a thread
-// owns 8 consecutive columns (one 16-byte load and one exponent per slot).
-__global__ __launch_bounds__(256) void moe_combine_h_kernel(const uint16_t* __restrict__ Yh,
-                                                            const int8_t* __restrict__ yexp,
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr);
+// out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] * 2^psig + w[t, k] * b2[e] ), slots in k
+// order, Y in the 24-bit float form the packed down GEMM writes (w * glu W2, without the bias; psig only
+// when some glu row was stored scaled). One workgroup per token; a thread owns 8 consecutive columns
+// (two 12-byte loads per slot).
+__global__ __launch_bounds__(256) void moe_combine_h_kernel(const unsigned char* __restrict__ Yb,
                                                             const int32_t* __restrict__ idx, uint16_t* __restrict__ out,
-                                                            int T, int K, int E, int H) {
-    const int t = blockIdx.x, NFH = H / 32;
+                                                            int T, int K, int E, int H,
+                                                            const int32_t* __restrict__ sync,
+                                                            const int8_t* __restrict__ psig,
+                                                            const float* __restrict__ bias, const float* __restrict__ route_w) {
+    const int t = blockIdx.x;
+    const bool scaled = sync[1] != 0;  // some glu row was stored scaled: its Y row is scaled by 2^-psig
     for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
         f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
         for (int k = 0; k < K; ++k) {
             const int e = idx[t * K + k];
             if ((unsigned)e >= (unsigned)E) continue;
-            const long long p = (long long)t * K + k;
-            const u32x4 v = *reinterpret_cast<const u32x4*>(Yh + p * H + 8 * c);
-            const int ex = yexp[p * NFH + (8 * c) / 32];
-            auto h = [&](uint32_t w, int hi) {
-                return __builtin_amdgcn_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(hi ? w >> 16 : w & 0xffffu)), ex);
-            };
-            s0 += f32x4{h(v[0], 0), h(v[0], 1), h(v[1], 0), h(v[1], 1)};
-            s1 += f32x4{h(v[2], 0), h(v[2], 1), h(v[3], 0), h(v[3], 1)};
+            const unsigned char* src = Yb + (((long long)t * K + k) * H + 8 * c) * 3;
+            f24x4 q0, q1;
+            __builtin_memcpy(&q0, src, 12);
+            __builtin_memcpy(&q1, src + 12, 12);
+            f32x4 y0 = unpack_f24x4(q0), y1 = unpack_f24x4(q1);
+            if (scaled) {
+                const float sc = __builtin_amdgcn_ldexpf(1.0f, psig[(long long)t * K + k]);
+                y0 *= sc;
+                y1 *= sc;
+            }
+            if (bias) {  // the slot's share of the down bias, w * b[e]
+                const float w = route_w[(long long)t * K + k];
+                const f32x4* b = reinterpret_cast<const f32x4*>(bias + (long long)e * H + 8 * c);
+                y0 += w * b[0];
+                y1 += w * b[1];
+            }
+            s0 += y0;
+            s1 += y1;
         }
         *reinterpret_cast<u32x4*>(out + (long long)t * H + 8 * c) =
             u32x4{pack_bf16x2(s0[0], s0[1]), pack_bf16x2(s0[2], s0[3]), pack_bf16x2(s1[0], s1[1]), pack_bf16x2(s1[2], s1[3])};
+    }
+}
+
+// Between the GEMMs: glu rows with a segment stored scaled (rsig[r] != 0, marked by GEMM1) are brought
+// to the row's largest segment scale s_r (the other segments rescaled by 2^-(s_r - s_u), fp16 round
+// to nearest); rsig[r] = s_r (GEMM2 scales a bias by 2^-s_r for that row) and psig[pair] = s_r for
+// every valid pair (the combine multiplies the pair's Y row by 2^s_r). Exits at once unless GEMM1
+// marked some row (sync[1]).
+__global__ __launch_bounds__(256) void moe_glu_fixup_kernel(uint16_t* __restrict__ glu, const int8_t* __restrict__ gexp,
+                                                            int8_t* __restrict__ rsig, int8_t* __restrict__ psig,
+                                                            const int32_t* __restrict__ sorted_pairs,
+                                                            const int32_t* __restrict__ sync,
+                                                            const int32_t* __restrict__ meta, int p_cap, int F) {
+    if (sync[1] == 0) return;
+    const int nrows = meta[1], U16 = F / 16;
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < nrows; r += gridDim.x * blockDim.x) {
+        if (rsig[r] == 0) {
+            psig[sorted_pairs[r]] = 0;
+            continue;
+        }
+        int smax = 0;
+        for (int u = 0; u < U16; ++u) smax = max(smax, (int)gexp[(long long)u * p_cap + r]);
+        for (int u = 0; u < U16; ++u) {
+            const int d = smax - gexp[(long long)u * p_cap + r];
+            if (d == 0) continue;
+            uint16_t* g = glu + (long long)r * F + 16 * u;
+            for (int j = 0; j < 16; ++j) {
+                const float v = (float)__builtin_bit_cast(_Float16, g[j]);
+                g[j] = __builtin_bit_cast(uint16_t, (_Float16)__builtin_amdgcn_ldexpf(v, -d));
+            }
+        }
+        rsig[r] = (int8_t)smax;
+        psig[sorted_pairs[r]] = (int8_t)smax;
     }
 }
 
@@ -672,13 +856,13 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  const int32_t* idx, const float* route_w, int T, int H, int F, int E, int K,
                                  int bias_interleaved, int act, void* out, int32_t* offsets, int32_t* tile_offsets,
                                  int32_t* meta, int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts,
-                                 int max_tiles, uint16_t* glu, float* Y, int8_t* yexp, hipStream_t s,
-                                 hipEvent_t* ev) {
+                                 int max_tiles, uint16_t* glu, float* Y, int8_t* gexp, int8_t* rsig,
+                                 int8_t* psig, hipStream_t s, hipEvent_t* ev) {
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     mark(0);
     hipError_t st =
         launch_route(idx, T, K, E, kPkBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts,
-                     meta + 8, s);
+                     meta + 8, s, rsig);
     if (st != hipSuccess) return st;
     mark(1);
     PkParams g1{};
@@ -703,6 +887,10 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.bias_interleaved = bias_interleaved;
     g1.a_bytes = T * H * 2;
     g1.counters = meta + 8;
+    g1.gexp = gexp;
+    g1.rsig = rsig;
+    g1.sync = meta + 24;
+    g1.p_cap = T * K;
     if (act == kActSilu)
         st = b1 ? launch_pk_t<kModePkGateUp, kActSilu, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActSilu, false>(g1, max_tiles, s);
@@ -716,25 +904,28 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     else
         st = launch_pk_t<kModePkUp, kActRelu, false>(g1, max_tiles, s);
     if (st != hipSuccess) return st;
+    hipLaunchKernelGGL(moe_glu_fixup_kernel, dim3(32), dim3(256), 0, s, glu, gexp, rsig, psig, sorted_pairs, meta + 24,
+                       meta, T * K, F);
+    st = hipGetLastError();
+    if (st != hipSuccess) return st;
     mark(2);
     PkParams g2 = g1;
     g2.A = glu;
     g2.B = static_cast<const uint16_t*>(w2p);
-    g2.bias = b2;
-    g2.out = Y;  // written as fp16 row segments (half of the fp32 buffer) with exponents in yexp
-    g2.yexp = yexp;
+    g2.out = Y;  // written as 24-bit floats (3/4 of the fp32 buffer)
+    g2.wexp = reinterpret_cast<const int8_t*>(static_cast<const uint16_t*>(w2p) + (long long)E * H * F);
     g2.Kd = F;
     g2.NF = H / 32;
     g2.KS = F / 16;
     g2.fw = pick_fw((long long)T * K, E, g2.NF, F, pk_cu_count());
     g2.counters = meta + 16;
     g2.n_tiles = ceil_div(g2.NF, g2.fw);
-    st = b2 ? launch_pk_t<kModePkDown, kActSilu, true>(g2, max_tiles, s)
-            : launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
+    g2.bias = nullptr;  // the down bias is added by the combine
+    st = launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(3);
-    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(256), 0, s, reinterpret_cast<const uint16_t*>(Y), yexp, idx,
-                       static_cast<uint16_t*>(out), T, K, E, H);
+    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(256), 0, s, reinterpret_cast<const unsigned char*>(Y), idx,
+                       static_cast<uint16_t*>(out), T, K, E, H, meta + 24, psig, b2, route_w);
     st = hipGetLastError();
     mark(4);
     return st;

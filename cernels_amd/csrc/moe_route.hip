@@ -90,9 +90,9 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_count_kernel(const int32
     for (int i = tid; i < E; i += kRtThreads) counts[(long long)blockIdx.x * E + i] = h[i];
 }
 
-// Work counters of the grouped GEMMs that follow the route (zeroed here, so that no launch of its own
-// is needed): kSchedInts ints, or none when sched is null.
-constexpr int kSchedInts = 16;
+// Work counters and completion flags of the grouped GEMMs that follow the route (zeroed here, so that
+// no launch of its own is needed): kSchedInts ints, or none when sched is null.
+constexpr int kSchedInts = 24;
 
 __global__ __launch_bounds__(kRouteThreads) void moe_route_scan_kernel(int32_t* __restrict__ counts, int ntiles, int E,
                                                                         int BM, int32_t* __restrict__ offsets,
@@ -134,7 +134,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_scan_kernel(int32_t* 
 
 __global__ __launch_bounds__(kRtThreads) void moe_route_scatter_kernel(const int32_t* __restrict__ idx, int T, int K,
                                                                          int E, const int32_t* __restrict__ bases,
-                                                                         int32_t* __restrict__ sorted_pairs) {
+                                                                         int32_t* __restrict__ sorted_pairs,
+                                                                         int8_t* __restrict__ row_zero) {
     extern __shared__ int32_t wh[];  // [4][E]: per-wave counts, then per-wave write cursors
     constexpr int kW = kRtThreads / kWave;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave, P = T * K;
@@ -182,6 +183,7 @@ __global__ __launch_bounds__(kRtThreads) void moe_route_scatter_kernel(const int
         if (valid) {
             const int k = q / T, t = q - k * T;
             sorted_pairs[base + rank] = t * K + k;
+            if (row_zero) row_zero[base + rank] = 0;
         }
         __builtin_amdgcn_wave_barrier();
         if (valid && rank == n_same - 1) wh[w * E + e] = base + n_same;
@@ -278,7 +280,7 @@ constexpr int kRtOneCells = 39 * 1024;  // LDS cells: ntiles * E histograms + 16
 __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     const int32_t* __restrict__ idx, int T, int K, int E, int BM, int ntiles, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
-    int32_t* __restrict__ meta, int32_t* __restrict__ sched) {
+    int32_t* __restrict__ meta, int32_t* __restrict__ sched, int8_t* __restrict__ row_zero) {
     extern __shared__ int32_t rt_lds[];
     int32_t* h = rt_lds;                    // [ntiles][E]
     int32_t* wc = rt_lds + ntiles * E;      // [16][E] per-wave counts, then cursors
@@ -370,7 +372,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     }
     if (valid) {
         const int k = div_by_t(q, T, rT), t = q - k * T;
-        sorted_pairs[wc[w * E + eq] + __popcll(m & lt_mask)] = t * K + k;
+        const int pos = wc[w * E + eq] + __popcll(m & lt_mask);
+        sorted_pairs[pos] = t * K + k;
+        if (row_zero) row_zero[pos] = 0;
     }
 }
 
@@ -379,7 +383,7 @@ size_t route_workspace_bytes(int T, int K, int E) { return (size_t)max(route_til
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream) {
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero) {
     const int nt = route_tiles(T, K);
     if (nt > 0 && (long long)(nt + kRouteWaves) * E <= kRtOneCells) {
         static bool lds_attr = false;  // dynamic LDS above 64 KiB must be allowed once per process
@@ -392,7 +396,7 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
         }
         hipLaunchKernelGGL(moe_route_one_kernel, dim3(nt), dim3(kRouteThreads),
                            (size_t)(nt + kRouteWaves) * E * sizeof(int32_t), stream, idx, T, K, E, BM, nt, offsets,
-                           sorted_pairs, tile_offsets, tile_expert, meta, sched);
+                           sorted_pairs, tile_offsets, tile_expert, meta, sched, row_zero);
         return hipGetLastError();
     }
     if ((long long)nt * E <= kRtFusedCells) {
@@ -406,7 +410,7 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
     }
     if (nt > 0)
         hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nt), dim3(kRtThreads), 4 * E * sizeof(int32_t), stream, idx,
-                           T, K, E, counts, sorted_pairs);
+                           T, K, E, counts, sorted_pairs, row_zero);
     return hipGetLastError();
 }
 

@@ -116,8 +116,9 @@ def moe_experts(
 class PackedExperts:
     """Expert weights re-laid once in MFMA-fragment order for the packed prefill entry.
 
-    ``gate_up`` / ``down`` hold the packed projections (bf16 tensors with the source element
-    count); biases are kept fp32 in their original column order (``bias_layout``).
+    ``gate_up`` / ``down`` hold the packed projections (uint8 buffers from ``pack_weights``: bf16
+    fragments, fp16 fragments plus a power-of-two table for the down projection); biases are kept
+    fp32 in their original column order (``bias_layout``).
     """
 
     def __init__(self, gate_up, down, H, F, E, act, bias_layout, gate_up_bias=None, down_bias=None):
@@ -131,19 +132,20 @@ def pack_weights(weight: torch.Tensor, layout: int, which: int, H: int, F: int,
                  out: torch.Tensor | None = None) -> torch.Tensor:
     """One projection of every expert, packed by cernels_moe_pack_weights (runs on weight's stream).
 
-    Each expert's packed block is contiguous and expert-major, so packing experts [0, a) and [a, b)
-    into consecutive slices of one buffer equals packing [0, b) at once (``out`` is such a slice).
+    The result is a uint8 buffer of ``cernels_moe_packed_weight_bytes`` bytes: the source's element
+    count for the first projections (bf16), and for DOWN the fp16 fragments followed by a table of one
+    power of two per expert and 32-column fragment.
     """
     _require(weight.is_cuda and weight.dtype == torch.bfloat16 and weight.is_contiguous() and weight.dim() == 3,
              "weight must be a contiguous bf16 CUDA tensor [E, ., .]")
     E = int(weight.size(0))
     L = _native.lib()
     nbytes = L.cernels_moe_packed_weight_bytes(H, F, E, which)
-    _require(nbytes > 0 and nbytes == weight.numel() * 2, f"cannot pack H={H} F={F} (need H % 64 == 0, F % 64 == 0)")
+    _require(nbytes >= weight.numel() * 2, f"cannot pack H={H} F={F} (need H % 64 == 0, F % 64 == 0)")
     if out is None:
-        out = torch.empty(weight.numel(), dtype=torch.bfloat16, device=weight.device)
-    _require(out.dtype == torch.bfloat16 and out.is_contiguous() and out.numel() == weight.numel()
-             and out.device == weight.device, "out must be a contiguous bf16 buffer of the weight's size")
+        out = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
+    _require(out.dtype == torch.uint8 and out.is_contiguous() and out.numel() == nbytes
+             and out.device == weight.device, "out must be a contiguous uint8 buffer of the packed size")
     with torch.cuda.device(weight.device):
         st = L.cernels_moe_pack_weights(_ptr(weight), H, F, E, layout, which, _ptr(out), _stream(weight.device))
     check(st, "cernels_moe_pack_weights")
@@ -179,12 +181,8 @@ def pack_experts_with_shared(gate_up_proj, down_proj, shared_gate, shared_up, sh
     F = F2 // 2
     sgu, sdn = split_shared_expert(shared_gate, shared_up, shared_down, F)
     S = int(sgu.shape[0])
-    gu = torch.empty(gate_up_proj.numel() + sgu.numel(), dtype=torch.bfloat16, device=gate_up_proj.device)
-    dn = torch.empty(down_proj.numel() + sdn.numel(), dtype=torch.bfloat16, device=down_proj.device)
-    pack_weights(gate_up_proj.contiguous(), LAYOUT_CONCAT, _native.GATE_UP, H, F, out=gu[:gate_up_proj.numel()])
-    pack_weights(sgu, LAYOUT_CONCAT, _native.GATE_UP, H, F, out=gu[gate_up_proj.numel():])
-    pack_weights(down_proj.contiguous(), LAYOUT_CONCAT, _native.DOWN, H, F, out=dn[:down_proj.numel()])
-    pack_weights(sdn, LAYOUT_CONCAT, _native.DOWN, H, F, out=dn[down_proj.numel():])
+    gu = pack_weights(torch.cat([gate_up_proj, sgu], dim=0).contiguous(), LAYOUT_CONCAT, _native.GATE_UP, H, F)
+    dn = pack_weights(torch.cat([down_proj, sdn], dim=0).contiguous(), LAYOUT_CONCAT, _native.DOWN, H, F)
     return PackedExperts(gu, dn, H, F, E + S, ACT_SILU, LAYOUT_CONCAT), S
 
 

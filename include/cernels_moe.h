@@ -104,10 +104,14 @@ int cernels_moe_experts_staged(const void* x, const void* gate_up_proj, const fl
  * into MFMA-fragment order (each 32x16 operand fragment is 1 KB of contiguous memory in the order
  * a 64-lane wave reads it). A model packs its expert weights once at load time, as the reference's
  * gpt-oss loader caches converted copies of its expert tensors (src/kops/registry/gpt_oss_moe_experts.py:14-26);
- * every later call streams them sequentially. Packing keeps the element count (2FH and HF per
- * expert) and accepts either source layout; the packed format no longer depends on the source
- * layout. No counterpart op in the reference: these entries are the fast path behind the same
- * loaders.
+ * every later call streams them sequentially. GATE_UP and UP keep bf16 and the element count (2FH
+ * and HF per expert). DOWN is stored as fp16 (the second projection multiplies fp16 activations,
+ * 2^-11 rounding instead of bf16's 2^-8), each 32-output-column fragment scaled by a power of two
+ * so its largest |w| lies in [2^14, 2^15); the fp16 fragments (HF per expert) are followed by a
+ * table of those powers (one int8 per expert and fragment, padded to 256 bytes). Size with
+ * cernels_moe_packed_weight_bytes. Either source layout is accepted; the packed format does not
+ * depend on it. No counterpart op in the reference: these entries are the fast path behind the
+ * same loaders.
  *   which: CERNELS_MOE_GATE_UP (src [E,2F,H] concat or [E,H,2F] interleaved), CERNELS_MOE_DOWN
  *          (src [E,H,F] concat or [E,F,H] interleaved) or CERNELS_MOE_UP (non-gated first projection,
  *          src [E,F,H] concat or [E,H,F] interleaved, i.e. megablocks' w1).

@@ -111,7 +111,7 @@ def experts_fp64(x, top_k_index, top_k_weights, gate_up_proj, down_proj, gate_up
     d = torch.float64
     x, w = x.to(d), top_k_weights.to(d)
     E = gate_up_proj.shape[0]
-    out = torch.zeros(x.shape, dtype=d)
+    out = torch.zeros(x.shape, dtype=d, device=x.device)
     idx = _valid_mask_index(top_k_index, E)
     for e in torch.unique(idx).tolist():
         if e == E:
@@ -219,7 +219,7 @@ def megablocks_fp64(x, top_k_index, top_k_weights, w1, w2, act_id: int):
     act = MEGABLOCKS_ACT_FNS[int(act_id)]
     x, w = x.to(d), top_k_weights.to(d)
     E = w1.shape[0]
-    out = torch.zeros(x.shape, dtype=d)
+    out = torch.zeros(x.shape, dtype=d, device=x.device)
     idx = _valid_mask_index(top_k_index, E)
     for e in torch.unique(idx).tolist():
         if e == E:
