@@ -67,6 +67,10 @@ _SIGNATURES = {
     "cernels_moe_decode_max_tokens": (_I, []),
     "cernels_moe_decode_max_pairs": (_I, []),
     "cernels_moe_experts_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I]),
+    "cernels_moe_experts_decode_noalloc": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
+    ),
     "cernels_moe_experts_decode": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _S, _P],

@@ -26,6 +26,8 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
                           int32_t* sorted_pairs, int32_t* tile_expert, int32_t* route_counts, int max_tiles,
                           uint16_t* glu, float* Y, hipStream_t s, hipEvent_t* ev);
 bool decode_shape_supported(int H, int F);
+size_t decode_noalloc_bytes();
+hipError_t decode_noalloc_scratch(void** ptr);
 int decode_max_pairs();
 int decode_max_tokens();
 size_t packed_weight_bytes(int H, int F, int E, int which);
@@ -353,6 +355,22 @@ int cernels_moe_experts_decode(const void* x, const void* gate_up_proj, const fl
                                hipStream_t stream) {
     return cernels_moe_experts_decode_staged(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights,
                                              T, H, F, E, K, layout, act, out, workspace, workspace_bytes, stream,
+                                             nullptr);
+}
+
+int cernels_moe_experts_decode_noalloc(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                                       const void* down_proj, const float* down_bias, const int32_t* indices,
+                                       const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                                       int32_t layout, int32_t act, void* out, hipStream_t stream) {
+    // The library's static per-GPU scratch takes the place of the workspace; every check of the decode
+    // entry applies (a shape it accepts always fits the scratch; the size check stays as a guard).
+    if (!dims_ok(T, H, F, E, K)) return CERNELS_MOE_INVALID_ARGUMENT;
+    if (T == 0) return CERNELS_MOE_OK;
+    if (decode_ws(T, H, F, K).total > cmoe::decode_noalloc_bytes()) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
+    void* ws = nullptr;
+    if (cmoe::decode_noalloc_scratch(&ws) != hipSuccess) return CERNELS_MOE_HIP_ERROR;
+    return cernels_moe_experts_decode_staged(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights,
+                                             T, H, F, E, K, layout, act, out, ws, cmoe::decode_noalloc_bytes(), stream,
                                              nullptr);
 }
 

@@ -13,6 +13,8 @@
 //
 // Layout: concat only (gate_up [E, 2F, H], down [E, H, F]); the reference has no decode entry
 // for the interleaved gpt-oss layout either.
+#include <mutex>
+
 #include "moe_common.h"
 
 namespace cmoe {
@@ -455,6 +457,39 @@ hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1,
     st = hipGetLastError();
     mark(2);
     return st;
+}
+
+// ---- scratch of the allocation-free decode entry (cernels_moe_experts_decode_noalloc) --------------
+// The workspace of the largest decode call the entry accepts: glu [kDecMaxPairs, 4096] bf16, then the
+// expert-sorted pair order [kDecMaxPairs] int32, laid out as the decode workspace is (moe_capi.cpp,
+// sections 256-byte aligned). Every GPU the library runs on holds its own copy until the process ends.
+// The decode kernels write every byte they read from it, so nothing needs clearing between calls;
+// calls that overlap on one GPU share it and race.
+constexpr size_t kDecNoAllocBytes = (size_t)kDecMaxPairs * 4096 * 2 + (size_t)kDecMaxPairs * 4;
+static __device__ __align__(256) unsigned char scratch[kDecNoAllocBytes];
+
+size_t decode_noalloc_bytes() { return kDecNoAllocBytes; }
+
+// This GPU's address of `scratch` (in host code the name is only a stand-in, not a device address):
+// looked up with hipGetSymbolAddress once per device, with that device current, and kept.
+hipError_t decode_noalloc_scratch(void** ptr) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t st = hipGetDevice(&dev);
+    if (st != hipSuccess) return st;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        void* p = nullptr;
+        st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (st != hipSuccess) return st;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 }  // namespace cmoe

@@ -156,6 +156,20 @@ int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, c
                                       int32_t layout, int32_t act, void* out, void* workspace,
                                       size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events);
 
+/* Allocation-free decode. No counterpart in the reference: for callers that cannot allocate device
+ * memory or pass a workspace (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments and result as cernels_moe_experts_decode without the workspace:
+ * the library keeps one static scratch of CERNELS_MOE_DECODE_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends) and calls no allocating routine. Every shape the decode entry accepts
+ * fits it (T*K <= cernels_moe_decode_max_pairs(), F <= 4096); a larger workspace need returns
+ * CERNELS_MOE_WORKSPACE_TOO_SMALL. Calls that overlap on one GPU share the scratch and race:
+ * serialise them (one stream, or events). */
+#define CERNELS_MOE_DECODE_NOALLOC_SCRATCH_BYTES (256u * 4096u * 2u + 256u * 4u)
+int cernels_moe_experts_decode_noalloc(const void* x, const void* gate_up_proj, const float* gate_up_bias,
+                                       const void* down_proj, const float* down_bias, const int32_t* indices,
+                                       const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
+                                       int32_t layout, int32_t act, void* out, hipStream_t stream);
+
 /* ---- router -------------------------------------------------------------------------------------
  * logits = bf16(x W^T + b) for x [T, H] bf16, W [E, H] bf16, b [E] bf16 (nullable), then per token:
  *   CERNELS_MOE_ROUTER_SOFTMAX_TOPK: softmax over the E logits in fp32, the K largest probabilities,
