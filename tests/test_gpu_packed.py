@@ -179,17 +179,21 @@ def test_packed_baseline_full_size(device, name):
     assert_within_tolerance(out.cpu(), ref_native.cpu().double(), f"{name} packed vs unpacked")
 
 
-@pytest.mark.parametrize("name", ["deepseek_v2_lite_prefill", "a3b_30b_prefill", "gpt_oss_20b_experts", "qwen3_next_zipf"])
+@pytest.mark.parametrize("name", ["deepseek_v2_lite_prefill", "a3b_30b_prefill", "gpt_oss_20b_experts", "qwen3_next_zipf",
+                                  "cohere2_moe_experts", "deepseek_ocr2_moe_experts"])
 def test_packed_full_output_strict(device, name):
-    """The north-star bar on the WHOLE [T, H] output of each BASELINE prefill workload, with no allowance:
-    max|out - exact| <= 2e-2 * RMS(exact), the exact value being the float64 restatement of the op on the
-    same bf16 inputs (computed on the GPU in float64 by the oracle; checker only). The correctly rounded
-    answer bf16(exact) is measured beside it, as the floor any bf16 output has."""
-    from cernels_amd.configs.registry import BASELINE_SHAPES
+    """The north-star bar on the WHOLE [T, H] output of each BASELINE prefill workload, and of the reference's
+    own prefill configs with their own routings (cohere2: top-k of the logits then sigmoid, no renorm,
+    src/configs/registry/cohere2_moe_experts.py:76-78; deepseek: softmax then top-k, no renorm,
+    deepseek_ocr2_moe_experts.py:80-83), with no allowance: max|out - exact| <= 2e-2 * RMS(exact), the
+    exact value being the float64 restatement of the op on the same bf16 inputs (computed on the GPU in
+    float64 by the oracle; checker only). The correctly rounded answer bf16(exact) is measured beside it,
+    as the floor any bf16 output has."""
+    from cernels_amd.configs.registry import BASELINE_SHAPES, REFERENCE_SHAPES
     from cernels_amd.configs.synth import make_inputs, make_weights
     from oracle import eager as O
 
-    s = BASELINE_SHAPES[name]
+    s = BASELINE_SHAPES.get(name) or REFERENCE_SHAPES[name]
     print(f"[strict full {name}] generating", flush=True)
     inp, wts = make_inputs(s), make_weights(s)
     c = dict(x=inp.x, idx=inp.top_k_index, w=inp.top_k_weights, W1=wts.gate_up_proj, W2=wts.down_proj,
@@ -202,9 +206,15 @@ def test_packed_full_output_strict(device, name):
                          layout=s.layout, act=s.act)
     rms = float(ref.pow(2).mean().sqrt())
     err = float((out - ref).abs().max()) / rms
+    print(f"[strict full {name}] max|exact|/RMS = {float(ref.abs().max()) / rms:.1f}", flush=True)
     floor = float((ref.to(torch.bfloat16).double() - ref).abs().max()) / rms
-    print(f"[strict full {name}] max|err|/RMS = {err:.4f} (correctly rounded bf16: {floor:.4f})", flush=True)
-    assert err <= 2e-2, f"{name}: max|err| = {err:.4f} RMS > 2e-2 RMS (bf16(exact) reads {floor:.4f})"
+    # The bar is 2e-2*RMS, or the correctly rounded answer's own max error where that is larger (no bf16
+    # output can do better; it happens on the reference's deepseek routing, whose weights are not
+    # renormalised).
+    bar = max(2e-2, floor)
+    print(f"[strict full {name}] max|err|/RMS = {err:.6f} (correctly rounded bf16: {floor:.6f}; bar {bar:.6f})",
+          flush=True)
+    assert err <= bar, f"{name}: max|err| = {err:.6f} RMS > {bar:.6f} RMS (bf16(exact) reads {floor:.6f})"
 
 
 def _scaled_rows_case(seed, T, H, Fi, E, K, big_rows, gain, bias=False):
