@@ -312,9 +312,57 @@ def route(indices: torch.Tensor, num_experts: int, tile_m: int = 128):
 
 
 # ---- the reference's per-model torch ops (same schemas) ---------------------------------------
+#
+# Prefill runs on packed weights: the first call with a given weight tensor packs it (one launch per
+# projection) and keeps the packed copy for as long as that tensor lives, keyed on its storage
+# pointer and in-place version counter (a write through ``.data`` does not advance the counter: call
+# ``forget_packed(gate_up_proj)`` after one). Decode reads the weights as stored.
+
+import weakref
+
+# id(gate_up_proj) -> (weakref to it, key, PackedExperts); an entry goes when its tensor is freed.
+# (Tensors compare elementwise, so a WeakKeyDictionary cannot key on them; identity is what is meant.)
+_PACKED: dict = {}
+
+
+def _packed_for(gate_up_proj, down_proj, layout, act, gate_up_bias=None, down_bias=None) -> PackedExperts:
+    key = tuple(None if t is None else (t.data_ptr(), t._version, tuple(t.shape))
+                for t in (gate_up_proj, down_proj, gate_up_bias, down_bias)) + (layout, act)
+    hit = _PACKED.get(id(gate_up_proj))
+    if hit is not None and hit[0]() is gate_up_proj and hit[1] == key:
+        return hit[2]
+    with torch.no_grad():
+        pk = pack_experts(gate_up_proj, down_proj, layout=layout, act=act, gate_up_bias=gate_up_bias,
+                          down_bias=down_bias)
+    tid = id(gate_up_proj)
+    ref = weakref.ref(gate_up_proj, lambda _r, tid=tid: _PACKED.pop(tid, None))
+    _PACKED[tid] = (ref, key, pk)
+    return pk
+
+
+def packed_copy(gate_up_proj) -> PackedExperts | None:
+    """The packed copy kept for ``gate_up_proj``, if any."""
+    hit = _PACKED.get(id(gate_up_proj))
+    return hit[2] if hit is not None and hit[0]() is gate_up_proj else None
+
+
+def forget_packed(gate_up_proj) -> None:
+    """Drop the packed copy kept for ``gate_up_proj`` (after a write through ``.data``)."""
+    if packed_copy(gate_up_proj) is not None:
+        _PACKED.pop(id(gate_up_proj), None)
+
+
+def _prefill_named(x, gate_up_proj, down_proj, indices, weights, topk, layout=LAYOUT_CONCAT, act=ACT_SILU,
+                   gate_up_bias=None, down_bias=None):
+    _check_inputs(x, gate_up_proj, down_proj, indices, weights, topk, layout, gate_up_bias, down_bias)
+    if x.shape[0] == 0:
+        return torch.empty((0, x.shape[1]), dtype=torch.bfloat16, device=x.device)
+    pk = _packed_for(gate_up_proj, down_proj, layout, act, gate_up_bias, down_bias)
+    return moe_experts_packed(x, pk, indices, weights, topk)
+
 
 def cohere2_moe_experts(x, gate_up_proj, down_proj, indices, weights, topk):
-    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk)
+    return _prefill_named(x, gate_up_proj, down_proj, indices, weights, topk)
 
 
 def cohere2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weights, topk):
@@ -322,7 +370,7 @@ def cohere2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weights, top
 
 
 def deepseek_ocr2_moe_experts(x, gate_up_proj, down_proj, indices, weights, topk):
-    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk)
+    return _prefill_named(x, gate_up_proj, down_proj, indices, weights, topk)
 
 
 def deepseek_ocr2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weights, topk):
@@ -330,12 +378,12 @@ def deepseek_ocr2_moe_experts_decode(x, gate_up_proj, down_proj, indices, weight
 
 
 def qwen3_next_moe_experts(x, gate_up_proj, down_proj, indices, weights, topk):
-    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk)
+    return _prefill_named(x, gate_up_proj, down_proj, indices, weights, topk)
 
 
 def gpt_oss_moe_experts(x, gate_up_proj, gate_up_bias, down_proj, down_bias, indices, weights, topk):
-    return moe_experts(x, gate_up_proj, down_proj, indices, weights, topk, layout=LAYOUT_INTERLEAVED, act=ACT_GPTOSS,
-                       gate_up_bias=gate_up_bias, down_bias=down_bias)
+    return _prefill_named(x, gate_up_proj, down_proj, indices, weights, topk, layout=LAYOUT_INTERLEAVED,
+                          act=ACT_GPTOSS, gate_up_bias=gate_up_bias, down_bias=down_bias)
 
 
 def pack_experts_nongated(w1: torch.Tensor, w2: torch.Tensor, act: int) -> PackedExperts:
@@ -386,6 +434,6 @@ __all__ = [
     "cohere2_moe_experts", "cohere2_moe_experts_decode",
     "deepseek_ocr2_moe_experts", "deepseek_ocr2_moe_experts_decode",
     "qwen3_next_moe_experts", "gpt_oss_moe_experts", "megablocks_moe", "pack_experts_nongated", "moe_router",
-    "split_shared_expert", "pack_experts_with_shared",
+    "split_shared_expert", "pack_experts_with_shared", "forget_packed", "packed_copy",
     "LAYOUT_CONCAT", "LAYOUT_INTERLEAVED", "ACT_SILU", "ACT_GPTOSS", "ACT_GELU_TANH", "ACT_SILU_PLAIN", "ACT_RELU",
 ]

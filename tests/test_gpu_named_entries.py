@@ -132,3 +132,26 @@ def test_named_megablocks_entry(device):
     _native.check(st, "cernels_megablocks_moe")
     torch.cuda.synchronize()
     assert_within_tolerance(out.cpu(), O.megablocks_fp64(x, idx, wt, w1, w2, act_id), "cernels_megablocks_moe")
+
+
+def test_python_named_ops_run_packed_and_cache(device):
+    """ops.<slug> (the reference's op names on the Python side) run prefill on a packed copy made on the
+    first call and kept per weight tensor; an in-place update of the weights (version bump) repacks. The
+    result meets the bar against the fp64 oracle and the reference's allclose against op_eager."""
+    from cernels_amd import ops
+
+    c = _golden_case("cohere2_t16")
+    d = dict(x=c["x"].to(device), W1=c["W1"].contiguous().to(device), W2=c["W2"].contiguous().to(device),
+             idx=c["idx"].to(torch.int32).to(device), w=c["w"].float().to(device))
+    out = ops.cohere2_moe_experts(d["x"], d["W1"], d["W2"], d["idx"], d["w"], d["idx"].shape[1]).cpu()
+    assert_reference_verify(out, c["eager"], "ops.cohere2_moe_experts")
+    assert_within_tolerance(out, oracle_fp64(c), "ops.cohere2_moe_experts")
+    pk = ops.packed_copy(d["W1"])
+    ops.cohere2_moe_experts(d["x"], d["W1"], d["W2"], d["idx"], d["w"], d["idx"].shape[1])
+    assert ops.packed_copy(d["W1"]) is pk  # reused
+    with torch.no_grad():
+        d["W2"].mul_(2.0)  # in-place: version bump, so the next call repacks
+    out2 = ops.cohere2_moe_experts(d["x"], d["W1"], d["W2"], d["idx"], d["w"], d["idx"].shape[1]).cpu()
+    assert ops.packed_copy(d["W1"]) is not pk
+    c2 = dict(c, W2=c["W2"] * 2.0)
+    assert_within_tolerance(out2, oracle_fp64(c2), "ops.cohere2_moe_experts after an in-place update")
