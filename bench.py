@@ -108,8 +108,9 @@ def stage_model(shape, U, P, stage, path="packed"):
     """Algorithmic FLOPs and HBM bytes of one launch of a stage (each distinct expert once).
 
     Y (the down GEMM's per-pair rows, read back by the combine) is 24-bit floats (3 bytes) on the packed
-    path and fp32 on the stored-layout path; glu is fp16 (packed) or bf16, 2 bytes either way, plus one
-    exponent byte per 16 glu columns on the packed path."""
+    path and fp32 on the stored-layout path; glu is fp16 (packed) or bf16, 2 bytes either way (the packed
+    path's exponent byte per 16 glu columns, P*F/16 bytes, is an implementation cost and not counted). The
+    gpt-oss down bias is counted with the down stage although the packed path's combine reads it."""
     T, H, F, E = shape.tokens, shape.hidden, shape.ffn, shape.experts
     if stage == "route":
         return 0.0, P * 4 * 2 + (E + 1) * 8
