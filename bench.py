@@ -488,117 +488,18 @@ def dense_gemm_calibration(dev, log, reps=20):
 
 REFERENCE_CONFIGS = ("cohere2_moe_experts", "cohere2_moe_experts_decode", "deepseek_ocr2_moe_experts",
                      "deepseek_ocr2_moe_experts_decode", "gpt_oss_moe_experts", "qwen3_next_moe_experts")
-REF_WARMUP = 10       # /root/reference/src/benchmark/main.py:20
-REF_MIN_RUN_S = 1.0   # blocked_autorange budget per workload (main.py:21)
 
 
-def _first(out):
-    return out[0] if isinstance(out, (tuple, list)) else out
+def run_reference_config(name, out_dir):
+    """One config through cernels_amd.benchmark (the reference's src/benchmark/main.py protocol: op_eager =
+    the transformers module, custom = the drop-in loader, verify, blocked_autorange), its record saved
+    under ``out_dir``; returns the record's workloads."""
+    from dataclasses import asdict
 
+    from cernels_amd.benchmark import main as runner
 
-def _transformers_module(name, cfg, standin, dev):
-    """The transformers module the reference's config calls as its op_eager baseline, built from its config
-    class with the config's shape and loaded with the same parameter tensors as the stand-in the drop-in
-    loader receives (so both workloads compute on identical weights). Eager experts dispatch."""
-    s = cfg.shape
-    if name.startswith("cohere2"):
-        from transformers.models.cohere2_moe.configuration_cohere2_moe import Cohere2MoeConfig
-        from transformers.models.cohere2_moe.modeling_cohere2_moe import Cohere2MoeExperts as cls
-        tc = Cohere2MoeConfig(hidden_size=s.hidden, intermediate_size=s.ffn, num_experts=s.experts,
-                              num_experts_per_tok=s.top_k, num_shared_experts=0, expert_selection_fn="sigmoid",
-                              norm_topk_prob=False, hidden_act="silu")
-    elif name.startswith("deepseek"):
-        from types import SimpleNamespace
-
-        from transformers.models.deepseek_ocr2.modeling_deepseek_ocr2 import DeepseekOcr2TextExperts as cls
-        tc = SimpleNamespace(num_experts=s.experts, hidden_size=s.hidden, moe_intermediate_size=s.ffn,
-                             hidden_act="silu")
-    elif name.startswith("gpt_oss"):
-        from transformers import GptOssConfig
-        from transformers.models.gpt_oss.modeling_gpt_oss import GptOssMLP as cls
-        tc = GptOssConfig(hidden_size=s.hidden, intermediate_size=s.ffn, num_local_experts=s.experts,
-                          num_experts_per_tok=s.top_k)
-    else:
-        from transformers import Qwen3NextConfig
-        from transformers.models.qwen3_next.modeling_qwen3_next import Qwen3NextSparseMoeBlock as cls
-        tc = Qwen3NextConfig(hidden_size=s.hidden, moe_intermediate_size=s.ffn, num_experts=s.experts,
-                             num_experts_per_tok=s.top_k, shared_expert_intermediate_size=cfg.shared_ffn,
-                             norm_topk_prob=True, hidden_act="silu")
-    import torch
-
-    tc._experts_implementation = "eager"
-    with torch.device(dev):
-        mod = cls(tc)
-    mod.load_state_dict({k: v for k, v in standin.state_dict().items() if v is not None}, strict=True)
-    return mod.to(dtype=cfg.dtype).eval()
-
-
-def _stats(times_ms, verified, ref_mean):
-    t = sorted(times_ms)
-    q = lambda f: t[min(len(t) - 1, int(f * (len(t) - 1) + 0.5))]  # noqa: E731
-    mean = statistics.mean(t)
-    return dict(mean_ms=mean, median_ms=statistics.median(t), min_ms=t[0], max_ms=t[-1], iqr_ms=q(0.75) - q(0.25),
-                n=len(t), verified=verified, speedup=None if ref_mean is None else ref_mean / mean)
-
-
-def run_reference_config(name, dev, log, out_dir):
-    """One config of the reference's benchmark runner (src/benchmark/main.py:29-63, record as save.py:47-77):
-    inputs -> op_eager (the transformers module on the GPU) -> warmup -> verify the custom workload against
-    op_eager with the config's allclose(2e-2) -> blocked_autorange timing of both -> a JSON record."""
-    import platform
-    import socket
-
-    import torch
-    from torch.utils.benchmark import Timer
-
-    from cernels_amd.configs.registry import CONFIGS
-
-    cfg = CONFIGS[name]
-    inputs = cfg.inputs(dev, cfg.dtype)
-    standin = inputs[-1]
-    op_eager_mod = _transformers_module(name, cfg, standin, dev)
-    if len(inputs) == 4:  # experts-level: (x, top_k_index, top_k_weights, experts)
-        baseline = lambda x, i, w, m: op_eager_mod(x, i, w)  # noqa: E731
-    else:  # module-level: (x, module)
-        baseline = lambda x, m: op_eager_mod(x)  # noqa: E731
-    workloads = {"op_eager": baseline, "custom": cfg.custom}
-    with torch.no_grad():
-        ref = _first(baseline(*inputs))
-    results, ref_mean = {}, None
-    for wl, fn in workloads.items():
-        with torch.no_grad():
-            for _ in range(REF_WARMUP):
-                fn(*inputs)
-            torch.cuda.synchronize()
-            verified = None if wl == "op_eager" else cfg.verify(_first(fn(*inputs)), ref)
-            m = Timer(stmt="fn(*inputs)", globals={"fn": fn, "inputs": inputs}).blocked_autorange(
-                min_run_time=REF_MIN_RUN_S)
-        times = [t * 1e3 for t in m.times]
-        results[wl] = _stats(times, verified, ref_mean)
-        if wl == "op_eager":
-            ref_mean = results[wl]["mean_ms"]
-        log(f"[{name}] {wl}: mean {results[wl]['mean_ms']:.4f} ms over {len(times)} samples x {m.number_per_run}"
-            + ("" if verified is None else f"; verify allclose(2e-2) vs op_eager: {verified}; "
-               f"speedup {results[wl]['speedup']:.1f}x"))
-    record = {
-        "timestamp": time.strftime("%Y-%m-%dT%H:%M:%S"),
-        "config": name,
-        "op": cfg.op,
-        "dtype": str(cfg.dtype).removeprefix("torch."),
-        "input_shapes": [list(t.shape) for t in cfg.inputs("meta", cfg.dtype) if hasattr(t, "shape")]
-        if len(inputs) == 4 else [list(inputs[0].shape)],
-        "machine": {"gpu": torch.cuda.get_device_name(0), "arch": platform.machine(),
-                    "backend": f"ROCm/HIP {torch.version.hip}", "torch": torch.__version__, "host": socket.gethostname()},
-        "reference": "op_eager",
-        "declared": {"op_eager": True, "op_compile": False, "hub": False, "lib": False, "custom": True},
-        "workloads": results,
-    }
-    out = Path(out_dir) / record["machine"]["host"]
-    out.mkdir(parents=True, exist_ok=True)
-    (out / f"{name}.json").write_text(json.dumps(record, indent=2))
-    del inputs, op_eager_mod, standin
-    torch.cuda.empty_cache()
-    return record
+    results = runner.main(name, root=out_dir)
+    return {w: asdict(r) for w, r in results.items()}
 
 
 # ---- HBM traffic per launch (rocprofv3 counters, child processes) ----------------------------------
@@ -707,11 +608,9 @@ def main():
     hip = _hip()
     if args.reference_configs:
         names = REFERENCE_CONFIGS if args.reference_configs == "all" else args.reference_configs.split(",")
-        recs = {n: run_reference_config(n, dev, log, ROOT / "gpurun_out" / "analysis") for n in names}
+        recs = {n: run_reference_config(n, ROOT / "gpurun_out" / "analysis") for n in names}
         print(json.dumps({"metric": "reference configs: custom vs op_eager (transformers module), ms per call",
-                          "unit": "ms", "higher_is_better": False, "n_gpus": 1,
-                          "configs": {n: {w: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in st.items()}
-                                          for w, st in r["workloads"].items()} for n, r in recs.items()}}), flush=True)
+                          "unit": "ms", "higher_is_better": False, "n_gpus": 1, "configs": recs}), flush=True)
         return
     if args.configs == "module":
         mods = {n: run_module_op(n, args.steps, args.warmup, dev, log) for n in MODULE_OPS}

@@ -15,6 +15,9 @@ Two families:
 
 from __future__ import annotations
 
+import weakref
+from types import SimpleNamespace
+
 import torch
 from torch import nn
 
@@ -79,6 +82,57 @@ REFERENCE_SHAPES: dict[str, MoeShape] = {
 }
 
 
+# stand-in module -> the transformers module built on its tensors (the op_eager baseline)
+_OP_EAGER: weakref.WeakKeyDictionary = weakref.WeakKeyDictionary()
+
+
+def op_eager_module(cfg: Config, standin: nn.Module) -> nn.Module:
+    """The transformers module a reference config calls as its op_eager baseline
+    (src/configs/registry/cohere2_moe_experts.py:99-104, deepseek_ocr2_moe_experts.py:100-105,
+    gpt_oss_moe_experts.py:55-62, qwen3_next_moe_experts.py:66-74): built from its transformers
+    config class at the config's shape, with the stand-in's own parameter tensors loaded (so the
+    baseline and the drop-in loader compute on identical weights), eager experts dispatch. Built once
+    per stand-in."""
+    mod = _OP_EAGER.get(standin)
+    if mod is not None:
+        return mod
+    s = cfg.shape
+    if isinstance(cfg, GptOssConfig):
+        from transformers import GptOssConfig as TC
+        from transformers.models.gpt_oss.modeling_gpt_oss import GptOssMLP as cls
+        tc = TC(hidden_size=s.hidden, intermediate_size=s.ffn, num_local_experts=s.experts,
+                num_experts_per_tok=s.top_k)
+    elif isinstance(cfg, Qwen3NextConfig):
+        from transformers import Qwen3NextConfig as TC
+        from transformers.models.qwen3_next.modeling_qwen3_next import Qwen3NextSparseMoeBlock as cls
+        tc = TC(hidden_size=s.hidden, moe_intermediate_size=s.ffn, num_experts=s.experts,
+                num_experts_per_tok=s.top_k, shared_expert_intermediate_size=cfg.shared_ffn,
+                norm_topk_prob=True, hidden_act="silu")
+    elif s.layout == LAYOUT_INTERLEAVED:  # experts-level gpt-oss
+        from transformers import GptOssConfig as TC
+        from transformers.models.gpt_oss.modeling_gpt_oss import GptOssExperts as cls
+        tc = TC(hidden_size=s.hidden, intermediate_size=s.ffn, num_local_experts=s.experts,
+                num_experts_per_tok=s.top_k)
+    elif s.name.startswith("deepseek"):
+        from transformers.models.deepseek_ocr2.modeling_deepseek_ocr2 import DeepseekOcr2TextExperts as cls
+        tc = SimpleNamespace(num_experts=s.experts, hidden_size=s.hidden, moe_intermediate_size=s.ffn,
+                             hidden_act="silu")
+    else:  # the cohere2 experts (the same forward serves the BASELINE experts-level shapes)
+        from transformers.models.cohere2_moe.configuration_cohere2_moe import Cohere2MoeConfig as TC
+        from transformers.models.cohere2_moe.modeling_cohere2_moe import Cohere2MoeExperts as cls
+        tc = TC(hidden_size=s.hidden, intermediate_size=s.ffn, num_experts=s.experts,
+                num_experts_per_tok=s.top_k, num_shared_experts=0, expert_selection_fn="sigmoid",
+                norm_topk_prob=False, hidden_act="silu")
+    tc._experts_implementation = "eager"
+    dev = next(standin.parameters()).device
+    with torch.device(dev):
+        mod = cls(tc)
+    mod.load_state_dict({k: v for k, v in standin.state_dict().items() if v is not None}, strict=True)
+    mod = mod.to(dtype=cfg.dtype).eval().requires_grad_(False)
+    _OP_EAGER[standin] = mod
+    return mod
+
+
 def experts_module(shape: MoeShape, device) -> Experts:
     w = make_weights(shape).to(device)
     return Experts(w.gate_up_proj, w.down_proj, w.gate_up_proj_bias, w.down_proj_bias)
@@ -92,6 +146,10 @@ class ExpertsConfig(Config):
         self.name = shape.name
         self.op = f"routed MoE experts T={shape.tokens} H={shape.hidden} F={shape.ffn} E={shape.experts} k={shape.top_k}"
         self.custom = custom
+
+    def baseline(self, x, top_k_index, top_k_weights, experts):
+        """op_eager: the transformers experts module on the same tensors."""
+        return op_eager_module(self, experts)(x, top_k_index, top_k_weights)
 
     def inputs(self, device, dtype=torch.bfloat16):
         if str(device) == "meta":
@@ -118,6 +176,10 @@ class GptOssConfig(Config):
         self.op = "GptOssMLP-shaped (router + clamped-SwiGLU grouped experts)"
         self.custom = staticmethod(_gpt_oss.kernel).__func__
 
+    def baseline(self, x, mlp):
+        """op_eager: transformers' GptOssMLP (router + experts) on the same tensors."""
+        return op_eager_module(self, mlp)(x)
+
     def inputs(self, device, dtype=torch.bfloat16):
         s = self.shape
         router = GptOssRouter(s.hidden, s.experts, s.top_k)
@@ -137,6 +199,10 @@ class Qwen3NextConfig(Config):
         self.shape, self.name = shape, shape.name
         self.op = "Qwen3NextSparseMoeBlock-shaped (router + grouped experts + gated shared expert)"
         self.custom = staticmethod(_qwen3.kernel).__func__
+
+    def baseline(self, x, block):
+        """op_eager: transformers' Qwen3NextSparseMoeBlock on the same tensors."""
+        return op_eager_module(self, block)(x)
 
     def inputs(self, device, dtype=torch.bfloat16):
         s = self.shape
@@ -158,6 +224,7 @@ class MegablocksConfig(Config):
     its attribute layout and router, with seeded N(0, 0.02) weights."""
 
     gated = False
+    reference_is_hub = True  # the reference's baseline is the Hub kernel, which needs the network
 
     def __init__(self):
         self.name = "megablocks_moe"
