@@ -14,7 +14,8 @@ Two correct bf16 implementations drift apart on a deep model too, so the same tw
 also measured between stock and stock under transformers' other experts implementation
 (``stock_drift_calibration``). The model is the real transformers architecture, from a local
 checkpoint directory or with seeded random weights (cernels_amd.modeling.models), fed seeded random
-token ids. The result is written as JSON (``--out``) and printed.
+token ids. The result is written as JSON to ``<out>/<host>/model/<model>.json`` (``--out``, default
+``analysis``; ``python -m cernels_amd.modeling.view`` tabulates the saved results) and printed.
 """
 
 from __future__ import annotations
@@ -159,7 +160,7 @@ def main(argv=None):
     ap.add_argument("--variants", help="comma list (stock is always first)")
     ap.add_argument("--stock-experts", choices=["default", "eager", "grouped_mm"], default="default",
                     help="transformers experts implementation of the stock variant")
-    ap.add_argument("--out", default="gpurun_out/model", help="directory for <model>.json")
+    ap.add_argument("--out", default="analysis", help="root of the saved results: <out>/<host>/model/<model>.json")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         sys.exit("modeling.main needs a GPU")
@@ -194,7 +195,7 @@ def main(argv=None):
         "machine": {"gpu": torch.cuda.get_device_name(0), "host": platform.node(), "torch": torch.__version__},
         "variants": results,
     }
-    out = Path(args.out)
+    out = Path(args.out) / payload["machine"]["host"] / "model"
     out.mkdir(parents=True, exist_ok=True)
     (out / f"{args.model}.json").write_text(json.dumps(payload, indent=1))
     print(json.dumps(payload, indent=1), flush=True)

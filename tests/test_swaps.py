@@ -185,3 +185,24 @@ def test_swapped_model_tracks_fp32_as_closely_as_stock(device):
     stock = [got["stock_grouped_mm"], got["stock_eager"]]
     assert got["custom"]["gate_prefix"] >= min(s["gate_prefix"] for s in stock), got
     assert got["custom"]["last_logits_max_diff"] <= 1.25 * max(s["last_logits_max_diff"] for s in stock), got
+
+
+def test_whole_model_results_table(tmp_path):
+    """modeling.view tabulates <root>/<host>/model/<model>.json, one row per variant."""
+    import json
+
+    from cernels_amd.modeling import view
+
+    d = tmp_path / "box" / "model"
+    d.mkdir(parents=True)
+    rec = {"model": "north_mini_code", "machine": {"gpu": "gfx950 test", "host": "box"},
+           "variants": {"stock": {"prefill_ms": 254.71, "decode_tok_s": 40.1, "generate_s": 3.2,
+                                  "gate_token_match": "64/64", "last_logits_max_diff": 0.0},
+                        "custom": {"prefill_ms": 51.12, "decode_tok_s": 51.8, "generate_s": 2.5,
+                                   "gate_token_match": "0/64", "last_logits_max_diff": 0.135}}}
+    (d / "north_mini_code.json").write_text(json.dumps(rec))
+    table = view.rows(tmp_path)
+    assert [r[2] for r in table[1:]] == ["stock", "custom"]
+    assert table[2][3:] == ["51.1", "51.80", "2.50", "0/64", "0.135"]
+    assert "north_mini_code" in view.main(tmp_path)
+    assert "no whole-model results" in view.main(tmp_path / "none")
