@@ -8,9 +8,13 @@ model in place and ``"stock"`` restores the class forward. Variants per model ar
 ``SWAPS`` in sweep order, stock first. Only the MoE-experts part of the reference's swaps is
 here; its SAM rel-pos and vision-tower variants are other kernels.
 
-Decode dispatch: calls with at most ``DECODE_MAX_TOKENS`` tokens use the decode GEMV. The
-reference switches at 4 (swaps.py:13). The gfx950 GEMV streams every distinct selected expert
-once, so it stays the faster entry up to the 8-token decode workload; the threshold is 8.
+Decode dispatch: a call uses the decode GEMV whenever the GEMV takes it (at most
+``DECODE_MAX_TOKENS`` tokens and ``DECODE_MAX_PAIRS`` routed (token, slot) pairs, the limits of
+``cernels_moe_experts_decode``), else the prefill GEMM. The reference switches at 4 tokens
+(swaps.py:13). The gfx950 GEMV streams every distinct selected expert once, so up to its limits it
+is the faster entry: measured through the ops with the weights rotated over three copies, 66 against
+98 us at 16 tokens and 95 against 109 us at 32 on the deepseek-v2-lite expert shapes (k=6), 135
+against 166 us and 183 against 212 us on the 30B-A3B shapes (k=8).
 """
 
 from __future__ import annotations
@@ -18,7 +22,13 @@ from __future__ import annotations
 from dataclasses import dataclass
 from importlib import import_module
 
-DECODE_MAX_TOKENS = 8
+DECODE_MAX_TOKENS = 64   # cernels_moe_decode_max_tokens()
+DECODE_MAX_PAIRS = 256   # cernels_moe_decode_max_pairs()
+
+
+def use_decode(tokens: int, top_k: int) -> bool:
+    """Whether a call of ``tokens`` tokens with ``top_k`` slots each goes to the decode GEMV."""
+    return tokens <= DECODE_MAX_TOKENS and tokens * top_k <= DECODE_MAX_PAIRS
 
 _REG = "cernels_amd.kops.registry."
 
@@ -56,7 +66,7 @@ def _dispatching_forward(module, prefill_op, decode_op):
     stock = type(module).forward
 
     def forward(hidden, top_k_index, top_k_weights):
-        op = decode_op if hidden.size(0) <= DECODE_MAX_TOKENS else prefill_op
+        op = decode_op if use_decode(hidden.size(0), top_k_index.size(-1)) else prefill_op
         if op is None:
             return stock(module, hidden, top_k_index, top_k_weights)
         return op(hidden, top_k_index, top_k_weights, module)

@@ -38,6 +38,9 @@ DECODE = [
     (5, 25, 2880, 2880, 32, 4, "silu", False, 0),
     (6, 2, 4096, 4096, 4, 2, "silu", False, 0),
     (7, 3, 136, 72, 5, 2, "silu", False, 0),
+    # the largest batches the swap dispatches to the GEMV, at the two models' expert shapes
+    (8, 32, 2048, 768, 128, 8, "silu", False, 0),
+    (9, 42, 1280, 896, 64, 6, "silu", False, 0),
 ]
 
 

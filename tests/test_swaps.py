@@ -30,9 +30,10 @@ class TinyModel(nn.Module):
         self.layers = nn.ModuleList([nn.ModuleDict({"experts": Cohere2MoeExperts(**kw)}) for _ in range(n)])
 
 
-def _calls(model, T):
+def _calls(model, T, K=8):
     h = torch.zeros(T, 4)
-    return [layer["experts"](h, None, None) for layer in model.layers]
+    idx = torch.zeros(T, K, dtype=torch.int64)
+    return [layer["experts"](h, idx, None) for layer in model.layers]
 
 
 def test_install_dispatch_and_restore():
@@ -41,8 +42,11 @@ def test_install_dispatch_and_restore():
     prefill = lambda h, i, w, mod: seen.append(("prefill", h.size(0), mod)) or "p"  # noqa: E731
     decode = lambda h, i, w, mod: seen.append(("decode", h.size(0), mod)) or "d"  # noqa: E731
     assert swaps.install(m, "Cohere2MoeExperts", prefill, decode) == 2
-    assert _calls(m, swaps.DECODE_MAX_TOKENS) == ["d", "d"]
-    assert _calls(m, swaps.DECODE_MAX_TOKENS + 1) == ["p", "p"]
+    # the decode GEMV takes every call within its limits: T <= 64 tokens and T*K <= 256 pairs
+    assert _calls(m, 32, K=8) == ["d", "d"]
+    assert _calls(m, 33, K=8) == ["p", "p"]
+    assert _calls(m, 64, K=4) == ["d", "d"]
+    assert _calls(m, 65, K=1) == ["p", "p"]
     assert seen[0][2] is m.layers[0]["experts"] and seen[1][2] is m.layers[1]["experts"]
     swaps.install(m, "Cohere2MoeExperts", prefill, None)  # prefill only: decode-sized calls stay stock
     assert _calls(m, 1) == [("stock", 1)] * 2
@@ -74,11 +78,12 @@ def test_swapped_module_matches_oracle(device):
     from helpers import assert_within_tolerance, rand_case
     from oracle import eager as O
 
-    c = rand_case(21, 40, 256, 128, 8, 2)
+    c = rand_case(21, 160, 256, 128, 8, 2)
     m = TinyModel(n=1, gate_up_proj=c["W1"], down_proj=c["W2"]).to(device)
     swaps.north_mini_code(m, "custom")
     ex = m.layers[0]["experts"]
-    for rows in (slice(0, 3), slice(None)):  # decode entry, then prefill entry
+    assert swaps.use_decode(3, 2) and not swaps.use_decode(160, 2)
+    for rows in (slice(0, 3), slice(None)):  # decode entry, then prefill entry (160 tokens x 2 slots > 256 pairs)
         out = ex(c["x"][rows].to(device), c["idx"][rows].to(device), c["w"][rows].to(device))
         ref = O.experts_fp64(c["x"][rows], c["idx"][rows], c["w"][rows], c["W1"], c["W2"])
         assert_within_tolerance(out.cpu(), ref, f"swapped rows {rows}")
@@ -206,3 +211,12 @@ def test_whole_model_results_table(tmp_path):
     assert table[2][3:] == ["51.1", "51.80", "2.50", "0/64", "0.135"]
     assert "north_mini_code" in view.main(tmp_path)
     assert "no whole-model results" in view.main(tmp_path / "none")
+
+
+def test_decode_limits_are_the_librarys():
+    """The swap's dispatch limits are the decode entry's own (host-side queries, no GPU call)."""
+    from cernels_amd import _native
+
+    L = _native.lib()
+    assert swaps.DECODE_MAX_TOKENS == L.cernels_moe_decode_max_tokens()
+    assert swaps.DECODE_MAX_PAIRS == L.cernels_moe_decode_max_pairs()
