@@ -10,9 +10,11 @@
 
 namespace cmoe {
 struct GemmParams;
+struct XcdSplit;
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr);
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr,
+                        const XcdSplit* split = nullptr);
 size_t route_workspace_bytes(int T, int K, int E);
 int gemm_tile_m();
 int packed_tile_m();
@@ -64,7 +66,8 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     size_t o = 0;
     w.offsets = o;      o = align_up(o + sizeof(int32_t) * (E + 1));
     w.tile_offsets = o; o = align_up(o + sizeof(int32_t) * (E + 1));
-    w.meta = o;         o = align_up(o + sizeof(int32_t) * 32);  // [0..1] route totals, [8..31] GEMM counters, flags
+    w.meta = o;         o = align_up(o + sizeof(int32_t) * 64);  // [0..1] route totals, [8..31] GEMM counters, flags,
+                                                                 // [32..49] per-XCD item ranges (packed)
     w.sorted_pairs = o; o = align_up(o + sizeof(int32_t) * P);
     w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
     w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));

@@ -127,4 +127,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __host__ __device__ constexpr int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Per-XCD item ranges of the two packed GEMMs (gate_up g = 0, down g = 1), written by the route
+// kernel once the expert histogram is known: XCD x of GEMM g takes items
+// [bounds[9g + x], bounds[9g + x + 1]). Shapes of the two launches are fixed by the host beforehand.
+struct XcdSplit {
+    int fw[2];        // fragments per item
+    int n_tiles[2];   // N-tiles (items per M-tile)
+    int slots[2];     // workgroups per XCD
+    int32_t* bounds;  // [2][9], or null: no split is written
+};
+
 }  // namespace cmoe

@@ -569,7 +569,8 @@ hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr);
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr,
+                        const XcdSplit* split = nullptr);
 
 // route -> gate_up GEMM -> down GEMM -> combine, all on stream s. Shapes were checked by the caller
 // (H % 64 == 0, F % 64 == 0, E <= 1024, T >= 1).

@@ -205,7 +205,7 @@ struct PkParams {
     const int32_t* offsets;        // [E+1]
     const int32_t* tile_offsets;   // [E+1]
     const int32_t* tile_expert;    // [tiles]
-    const int32_t* meta;           // [0] = M-tiles
+    const int32_t* bounds;         // [9] per-XCD item ranges, written by the route
     const float* route_w;          // [P] (GEMM2)
     void* out;                     // GEMM1: glu fp16 [P, F]; GEMM2: Y as 24-bit floats [P, H]
     int Kd, NF, KS, n_tiles;
@@ -250,17 +250,15 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
-    const int tiles = prm.meta[0];
-    const int total = tiles * prm.n_tiles;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
-    const int per = ceil_div(total, 8);
-    const int it_end = min(total, (xcd + 1) * per);
+    const int b_lo = prm.bounds[xcd], b_hi = prm.bounds[xcd + 1];
     const int Kd = prm.Kd, nst = Kd / kBK;
     const int a_chunk = tid & 7;
 
-    // Items of XCD x are [x*per, x*per + per), so that the items that share a weight tile
-    // (neighbours in the list) run at about the same time on one XCD's L2. Each slot of the XCD takes
-    // offsets s and 2*slots-1-s first (snake order: long and short items mix on every CU), then draws
+    // Items of XCD x are one contiguous range of the list, [bounds[x], bounds[x+1]) (moe_split.h: of
+    // about equal estimated cost, at most the rounds of an equal split), so that the items that share
+    // a weight tile (neighbours in the list) run at about the same time on one XCD's L2. Each slot of
+    // the XCD takes offsets s and 2*slots-1-s first (snake order: long and short items mix on every CU), then draws
     // offsets 2*slots + n from the XCD's work counter: workgroups that run faster take more items,
     // so the launch does not end on the slowest workgroup's fixed share. (Drawing from the other
     // XCDs' counters once the own one is exhausted was measured slower: the blocking draws and the
@@ -270,9 +268,9 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
         return true;
     };
-    auto item_of_off = [&](int x, int off) {  // item at offset off of XCD x, or -1
-        const int it = x * per + off;
-        return (off < per && it < min(total, (x + 1) * per)) ? it : -1;
+    auto item_of_off = [&](int off) {  // item at offset off of this XCD's range, or -1
+        const int it = b_lo + off;
+        return it < b_hi ? it : -1;
     };
     __shared__ int s_next;  // item after next (global index or -1), published once per item
     // Operands are read with buffer loads: a 128-bit descriptor per operand and item (uniform,
@@ -332,8 +330,8 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     };
 
     WorkItem cur;
-    if (!item_at(item_of_off(xcd, slot), cur)) return;
-    int it_nx = item_of_off(xcd, 2 * slots - 1 - slot);  // the next item
+    if (!item_at(item_of_off(slot), cur)) return;
+    int it_nx = item_of_off(2 * slots - 1 - slot);  // the next item
     // Thread 0 holds the counter ticket of the item after next: drawn one item ahead, so the
     // atomic's round trip is over long before its value is published.
     int ticket = 0;
@@ -555,7 +553,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         } else {
             dispatch(IC<0>{});
         }
-        if (tid == 0) s_next = item_of_off(xcd, 2 * slots + ticket);
+        if (tid == 0) s_next = item_of_off(2 * slots + ticket);
 
         // ---- epilogue: element r of a transposed 32x32 accumulator block is row lane & 31 of the
         // block, column 8*(r/4) + 4*(lane/32) + (r%4) of the fragment. Only LDS reads and global
@@ -731,10 +729,15 @@ static int pk_cu_count() {
     return g_pk_cu_count;
 }
 
+// Workgroups of a packed GEMM launch: one per CU, a multiple of 8 (the same count on every XCD).
+static int pk_grid(int max_tiles, int n_tiles) {
+    const int grid = min(max_tiles * n_tiles, pk_cu_count());
+    return ceil_div(max(grid, 1), 8) * 8;
+}
+
 template <int MODE, int ACT, bool HAS_BIAS>
 static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s) {
-    int grid = min(max_tiles * prm.n_tiles, pk_cu_count());  // one workgroup per CU
-    grid = ceil_div(max(grid, 1), 8) * 8;
+    const int grid = pk_grid(max_tiles, prm.n_tiles);
     const int nst = prm.Kd / kBK;
     if (nst >= 2 && (nst & 1) == 0)
         hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
@@ -747,7 +750,8 @@ static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s)
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr);
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr,
+                        const XcdSplit* split = nullptr);
 // out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] * 2^psig + w[t, k] * b2[e] ), slots in k
 // order, Y in the 24-bit float form the packed down GEMM writes (w * glu W2, without the bias; psig only
 // when some glu row was stored scaled). One workgroup per token; a thread owns 8 consecutive columns
@@ -859,10 +863,17 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  int max_tiles, uint16_t* glu, float* Y, int8_t* gexp, int8_t* rsig,
                                  int8_t* psig, hipStream_t s, hipEvent_t* ev) {
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
+    // Launch shapes of both GEMMs, from the shape alone; the route then splits each one's items over
+    // the XCDs (meta[32..40] gate_up, meta[41..49] down).
+    const int nf1 = act_is_gated(act) ? F / 16 : F / 32, nf2 = H / 32;
+    const int fw1 = pick_fw((long long)T * K, E, nf1, H, pk_cu_count());
+    const int fw2 = pick_fw((long long)T * K, E, nf2, F, pk_cu_count());
+    const int nt1 = ceil_div(nf1, fw1), nt2 = ceil_div(nf2, fw2);
+    XcdSplit split{{fw1, fw2}, {nt1, nt2}, {pk_grid(max_tiles, nt1) / 8, pk_grid(max_tiles, nt2) / 8}, meta + 32};
     mark(0);
     hipError_t st =
         launch_route(idx, T, K, E, kPkBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts,
-                     meta + 8, s, rsig);
+                     meta + 8, s, rsig, &split);
     if (st != hipSuccess) return st;
     mark(1);
     PkParams g1{};
@@ -873,14 +884,14 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.offsets = offsets;
     g1.tile_offsets = tile_offsets;
     g1.tile_expert = tile_expert;
-    g1.meta = meta;
+    g1.bounds = meta + 32;
     g1.route_w = route_w;
     g1.out = glu;
     g1.Kd = H;
-    g1.NF = act_is_gated(act) ? F / 16 : F / 32;
+    g1.NF = nf1;
     g1.KS = H / 16;
-    g1.fw = pick_fw((long long)T * K, E, g1.NF, H, pk_cu_count());
-    g1.n_tiles = ceil_div(g1.NF, g1.fw);
+    g1.fw = fw1;
+    g1.n_tiles = nt1;
     g1.F = F;
     g1.H = H;
     g1.topk = K;
@@ -915,11 +926,12 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.out = Y;  // written as 24-bit floats (3/4 of the fp32 buffer)
     g2.wexp = reinterpret_cast<const int8_t*>(static_cast<const uint16_t*>(w2p) + (long long)E * H * F);
     g2.Kd = F;
-    g2.NF = H / 32;
+    g2.NF = nf2;
     g2.KS = F / 16;
-    g2.fw = pick_fw((long long)T * K, E, g2.NF, F, pk_cu_count());
+    g2.fw = fw2;
     g2.counters = meta + 16;
-    g2.n_tiles = ceil_div(g2.NF, g2.fw);
+    g2.n_tiles = nt2;
+    g2.bounds = meta + 41;
     g2.bias = nullptr;  // the down bias is added by the combine
     st = launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;

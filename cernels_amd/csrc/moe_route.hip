@@ -19,6 +19,7 @@
 //                                     ranking lanes that share an expert with a bit-sliced ballot
 // The scattered 4-byte writes of the permutation are spread over many CUs.
 #include "moe_common.h"
+#include "moe_split.h"
 
 namespace cmoe {
 
@@ -50,6 +51,26 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wave_tot, int* t
     *total = wave_tot[kRouteWaves - 1];
     __syncthreads();  // wave_tot is reused by the next scan
     return before + x - v;
+}
+
+// Per-XCD item ranges of the packed GEMMs (moe_split.h), by all threads of the block: thread e
+// holds expert e's pairs run at off and its nt M-tiles of BM rows at toff. Each thread writes the
+// boundaries inside its expert (each of b[1..7] has exactly one writer when the list is not empty;
+// for an empty one the clamp makes every bound 0 whatever s_b holds), then two threads clamp and
+// store them.
+__device__ __forceinline__ void write_xcd_split(const XcdSplit& sp, int BM, int run, int nt, int off, int toff,
+                                                int valid_total, int tiles_total, int* s_b) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+        split_expert(sp.fw[g], sp.n_tiles[g], BM, run, nt, toff, off,
+                     32LL * sp.fw[g] * tiles_total + valid_total, s_b + 9 * g);
+    __syncthreads();
+    if (tid == 0 || tid == kWave) {
+        const int g = tid == 0 ? 0 : 1;
+        split_clamp(s_b + 9 * g, tiles_total * sp.n_tiles[g], sp.slots[g]);
+        for (int k = 0; k < 9; ++k) sp.bounds[9 * g + k] = s_b[9 * g + k];
+    }
 }
 
 constexpr int kRtTile = 1024;   // pairs per route tile
@@ -99,8 +120,9 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_scan_kernel(int32_t* 
                                                                         int32_t* __restrict__ tile_offsets,
                                                                         int32_t* __restrict__ tile_expert,
                                                                         int32_t* __restrict__ meta,
-                                                                        int32_t* __restrict__ sched) {
+                                                                        int32_t* __restrict__ sched, XcdSplit split) {
     __shared__ int wave_tot[kRouteWaves];
+    __shared__ int s_split[18];
     const int tid = threadIdx.x;
     const int e = tid;  // E <= kRouteThreads is checked on the host
     int run = 0;
@@ -116,6 +138,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_scan_kernel(int32_t* 
     const int off = block_exclusive_scan(run, wave_tot, &valid_total);
     const int nt = ceil_div(run, BM);
     const int toff = block_exclusive_scan(nt, wave_tot, &tiles_total);
+    if (split.bounds) write_xcd_split(split, BM, run, nt, off, toff, valid_total, tiles_total, s_split);
     if (e < E) {
         offsets[e] = off;
         tile_offsets[e] = toff;
@@ -200,9 +223,10 @@ constexpr int kRtFusedCells = 28 * 1024;
 __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     const int32_t* __restrict__ idx, int T, int K, int E, int BM, int ntiles, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
-    int32_t* __restrict__ meta, int32_t* __restrict__ sched) {
+    int32_t* __restrict__ meta, int32_t* __restrict__ sched, XcdSplit split) {
     __shared__ int32_t h[kRtFusedCells];  // [ntiles][E]
     __shared__ int wave_tot[kRouteWaves];
+    __shared__ int s_split[18];
     const int tid = threadIdx.x, P = T * K;  // P <= kRtFusedCells * kRtTile here, far below 2^31
     for (int i = tid; i < ntiles * E; i += kRouteThreads) h[i] = 0;
     __syncthreads();
@@ -252,6 +276,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     const int off = block_exclusive_scan(run, wave_tot, &valid_total);
     const int nt = ceil_div(run, BM);
     const int toff = block_exclusive_scan(nt, wave_tot, &tiles_total);
+    if (split.bounds) write_xcd_split(split, BM, run, nt, off, toff, valid_total, tiles_total, s_split);
     if (e < E) {
         offsets[e] = off;
         tile_offsets[e] = toff;
@@ -280,8 +305,9 @@ constexpr int kRtOneCells = 39 * 1024;  // LDS cells: ntiles * E histograms + 16
 __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     const int32_t* __restrict__ idx, int T, int K, int E, int BM, int ntiles, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ tile_offsets, int32_t* __restrict__ tile_expert,
-    int32_t* __restrict__ meta, int32_t* __restrict__ sched, int8_t* __restrict__ row_zero) {
+    int32_t* __restrict__ meta, int32_t* __restrict__ sched, int8_t* __restrict__ row_zero, XcdSplit split) {
     extern __shared__ int32_t rt_lds[];
+    __shared__ int s_split[18];
     int32_t* h = rt_lds;                    // [ntiles][E]
     int32_t* wc = rt_lds + ntiles * E;      // [16][E] per-wave counts, then cursors
     __shared__ int wave_tot[kRouteWaves];
@@ -336,6 +362,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     const int off = block_exclusive_scan(run, wave_tot, &valid_total);
     const int nt = ceil_div(run, BM);
     const int toff = block_exclusive_scan(nt, wave_tot, &tiles_total);
+    if (blockIdx.x == 0 && split.bounds) write_xcd_split(split, BM, run, nt, off, toff, valid_total, tiles_total, s_split);
     if (blockIdx.x == 0) {
         if (e < E) {
             offsets[e] = off;
@@ -383,8 +410,9 @@ size_t route_workspace_bytes(int T, int K, int E) { return (size_t)max(route_til
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
-                        int32_t* sched, hipStream_t stream, int8_t* row_zero) {
+                        int32_t* sched, hipStream_t stream, int8_t* row_zero, const XcdSplit* split) {
     const int nt = route_tiles(T, K);
+    const XcdSplit sp = split ? *split : XcdSplit{};
     if (nt > 0 && (long long)(nt + kRouteWaves) * E <= kRtOneCells) {
         static bool lds_attr = false;  // dynamic LDS above 64 KiB must be allowed once per process
         if (!lds_attr) {
@@ -396,17 +424,17 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
         }
         hipLaunchKernelGGL(moe_route_one_kernel, dim3(nt), dim3(kRouteThreads),
                            (size_t)(nt + kRouteWaves) * E * sizeof(int32_t), stream, idx, T, K, E, BM, nt, offsets,
-                           sorted_pairs, tile_offsets, tile_expert, meta, sched, row_zero);
+                           sorted_pairs, tile_offsets, tile_expert, meta, sched, row_zero, sp);
         return hipGetLastError();
     }
     if ((long long)nt * E <= kRtFusedCells) {
         hipLaunchKernelGGL(moe_route_count_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, idx, T, K, E, BM, nt,
-                           counts, offsets, tile_offsets, tile_expert, meta, sched);
+                           counts, offsets, tile_offsets, tile_expert, meta, sched, sp);
     } else {
         hipLaunchKernelGGL(moe_route_count_kernel, dim3(nt), dim3(kRtThreads), E * sizeof(int32_t), stream, idx, T, K,
                            E, counts);
         hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteThreads), 0, stream, counts, nt, E, BM, offsets,
-                           tile_offsets, tile_expert, meta, sched);
+                           tile_offsets, tile_expert, meta, sched, sp);
     }
     if (nt > 0)
         hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nt), dim3(kRtThreads), 4 * E * sizeof(int32_t), stream, idx,

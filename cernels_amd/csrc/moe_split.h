@@ -1,0 +1,64 @@
+// Per-XCD item ranges of the packed grouped GEMMs, balanced by estimated cost. Host and device
+// code: the route kernel evaluates it per expert, and a CPU test checks it against a brute-force
+// count over the item list (compiled there with CMOE_HD defined empty).
+//
+// The items of a packed GEMM are (M-tile, N-tile) pairs, listed expert by expert and N-tile-major
+// inside an expert. An item of r rows costs 32 fw + r, in bytes streamed through the CU per row of the
+// reduction over 32 columns (its fw weight fragments of 32 columns and its r activation rows). Expert
+// e's items cost n_tiles * (32 fw nt_e + run_e) together, so the cost before expert e is
+// n_tiles * (32 fw toff_e + off_e), from the two prefixes the route has already scanned. XCD x starts
+// at the first item whose cost prefix reaches ceil(x W / 8) of the total W. Then no range may hold more
+// than cap items: the rounds of items an equal split gives each workgroup,
+// r = ceil(ceil(items / 8) / slots), plus r / 8. Where rounds are few, one more item in a workgroup
+// costs a whole round, more than the balance gains; where they are many, the extra items are the
+// cheap ones.
+#pragma once
+
+#ifndef CMOE_HD
+#define CMOE_HD __host__ __device__
+#endif
+
+namespace cmoe {
+
+// floor(a / b) for 0 <= a, 0 < b, quotient < 2^20: a float estimate within one of the quotient
+// (relative error a few 2^-24), then one exact correction. Avoids the long 64-bit division sequence.
+CMOE_HD inline int split_floordiv(long long a, long long b) {
+    int q = (int)((float)a * (1.0f / (float)b));
+    const long long r = a - (long long)q * b;
+    return q + (r >= b ? 1 : 0) - (r < 0 ? 1 : 0);
+}
+
+// Writes b[k] for the boundaries k in 1..7 that fall inside one expert: run pairs in nt M-tiles of
+// bm rows, the first one toff, off pairs before it; W = 32 fw tiles + pairs of the whole list (the
+// cost of one N-tile of every expert).
+CMOE_HD inline void split_expert(int fw, int n_tiles, int bm, int run, int nt, int toff, int off, long long W,
+                                 int* b) {
+    if (nt <= 0) return;
+    const long long Wt = (long long)n_tiles * W;
+    const long long c = 32LL * fw * nt + run;  // cost of one N-tile of the expert
+    const long long S = (long long)n_tiles * (32LL * fw * toff + off), Se = S + n_tiles * c;
+    // boundary k lies in (S, Se]: S < ceil(k Wt / 8) <= Se, i.e. 8 S / Wt < k <= 8 Se / Wt
+    const int k0 = split_floordiv(8 * S, Wt) + 1, k1 = split_floordiv(8 * Se, Wt);
+    for (int k = k0 < 1 ? 1 : k0; k <= (k1 > 7 ? 7 : k1); ++k) {
+        const long long R = (k * Wt + 7) / 8 - S;  // 1 <= R <= n_tiles * c
+        const int n = split_floordiv(R - 1, c), r = (int)(R - n * c);
+        const int full = 32 * fw + bm;                // cost of a full M-tile; only the last one is partial
+        const int m = (r + full - 1) / full;          // M-tiles of N-tile n that start before the boundary
+        b[k] = toff * n_tiles + n * nt + (m < nt ? m : nt);
+    }
+}
+
+// b[1..7] from split_expert (0 where no expert wrote one: the list is empty) -> final bounds b[0..8].
+CMOE_HD inline void split_clamp(int* b, int total, int slots) {
+    const int rounds = ((total + 7) / 8 + slots - 1) / slots, cap = (rounds + rounds / 8) * slots;
+    b[0] = 0;
+    for (int k = 1; k < 8; ++k) {
+        int v = b[k];
+        v = v < b[k - 1] + cap ? v : b[k - 1] + cap;
+        v = v > total - (8 - k) * cap ? v : total - (8 - k) * cap;
+        b[k] = v > b[k - 1] ? v : b[k - 1];
+    }
+    b[8] = total;
+}
+
+}  // namespace cmoe

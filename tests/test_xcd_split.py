@@ -1,0 +1,139 @@
+"""The packed GEMMs' per-XCD item ranges (cernels_amd/csrc/moe_split.h), evaluated on the CPU.
+
+The route kernel computes them in integer and float arithmetic per expert; here the same header is
+compiled for the host and its bounds are compared with the definition counted item by item: XCD x
+starts at the first item whose cost prefix reaches ceil(x W / 8), an item of r rows costing
+32 fw + r. Where that split would give some XCD more than cap items (the R rounds an equal
+split gives each workgroup, plus R / 8) the bounds are clamped; every result covers the list once, in
+order, with at most cap items per XCD.
+"""
+
+from __future__ import annotations
+
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+@pytest.fixture(scope="module")
+def split_exe(tmp_path_factory):
+    exe = tmp_path_factory.mktemp("split") / "xcd_split_check"
+    subprocess.run(["g++", "-O2", "-std=c++17", "-DCMOE_HD=", "-I", str(ROOT / "cernels_amd" / "csrc"),
+                    str(ROOT / "tests" / "xcd_split_check.cpp"), "-o", str(exe)], check=True)
+    return exe
+
+
+def _run(exe, cases):
+    text = "".join(f"S {len(r)} {fw} {nt} {sl} " + " ".join(map(str, r)) + "\n" for r, fw, nt, sl in cases)
+    out = subprocess.run([str(exe)], input=text, capture_output=True, text=True, check=True).stdout
+    return [list(map(int, line.split())) for line in out.strip().splitlines()]
+
+
+def _by_definition(runs, fw, n_tiles):
+    """Unclamped bounds, counted over the item list (expert by expert, N-tile-major)."""
+    costs = []
+    for r in runs:
+        nt = -(-r // 256)
+        rows = np.minimum(256, r - 256 * np.arange(nt))
+        costs.append(np.tile(32 * fw + rows, n_tiles))
+    costs = np.concatenate(costs) if costs else np.zeros(0, np.int64)
+    start = np.concatenate([[0], np.cumsum(costs)])[:-1]
+    W = int(costs.sum())
+    return [int(np.searchsorted(start, -(-k * W // 8), side="left")) for k in range(9)], len(costs)
+
+
+def _cap(total, slots):
+    rounds = -(-(-(-total // 8)) // slots)
+    return (rounds + rounds // 8) * slots
+
+
+def _cases():
+    rng = np.random.default_rng(7)
+    cases = [([0] * 8, 8, 4, 32), ([1], 8, 1, 1), ([300], 1, 360, 32), ([256] * 64, 7, 8, 32),
+             ([384] * 64, 8, 8, 32), ([512] * 32, 8, 23, 32), ([0, 0, 5, 0], 3, 2, 1)]
+    for _ in range(300):
+        E = int(rng.integers(1, 300))
+        P = int(rng.integers(0, 60000))
+        runs = rng.multinomial(P, rng.dirichlet(np.full(E, rng.uniform(0.05, 3.0)))).tolist()
+        cases.append((runs, int(rng.integers(1, 9)), int(rng.integers(1, 48)), int(rng.integers(1, 33))))
+    return cases
+
+
+def _start_of(runs, fw, n_tiles, items):
+    """Cost prefix before each given item index, from the per-expert closed form."""
+    nt = -(-np.asarray(runs, np.int64) // 256)
+    c = 32 * fw * nt + np.asarray(runs, np.int64)
+    first = np.concatenate([[0], np.cumsum(nt * n_tiles)])
+    S = np.concatenate([[0], np.cumsum(n_tiles * c)])
+    items = np.asarray(items, np.int64)
+    e = np.searchsorted(first, items, side="right") - 1
+    e = np.minimum(e, len(runs) - 1)
+    local = items - first[e]
+    ntile = np.maximum(nt[e], 1)
+    n, m = local // ntile, local % ntile
+    return S[e] + n * c[e] + m * (32 * fw + 256), int(S[-1])
+
+
+def test_split_matches_the_item_count_definition(split_exe):
+    cases = _cases()
+    got = _run(split_exe, cases)
+    assert len(got) == len(cases)
+    clamped = 0
+    for (runs, fw, n_tiles, slots), b in zip(cases, got):
+        want, total = _by_definition(runs, fw, n_tiles)
+        cap = _cap(total, slots)
+        assert b[0] == 0 and b[8] == total and all(x <= y for x, y in zip(b, b[1:])), (runs[:8], b)
+        assert max(y - x for x, y in zip(b, b[1:])) <= cap, (b, cap)
+        if max(y - x for x, y in zip(want, want[1:])) <= cap:
+            assert b == want, (fw, n_tiles, slots, b, want)
+        else:
+            clamped += 1
+    assert clamped > 0  # the clamp is exercised too
+
+
+def test_equal_items_split_evenly(split_exe):
+    """Experts of equal size: the cost split is the equal item split."""
+    (b,) = _run(split_exe, [([256] * 64, 8, 8, 32)])
+    assert b == [64 * x for x in range(9)]
+
+
+def test_split_of_long_lists(split_exe):
+    """2^29 pairs and over: cost prefixes beyond 2^32. Each bound is the first item whose cost prefix
+    reaches ceil(x W / 8), checked at the bound and at the item before it (at this many rounds the
+    clamp does not bind)."""
+    rng = np.random.default_rng(11)
+    cases = [(rng.integers(0, 1 << 20, size=1024).tolist(), 1, 360, 32),
+             (rng.integers(0, 1 << 21, size=256).tolist(), 8, 23, 32)]
+    big = 0
+    for (runs, fw, n_tiles, slots), b in zip(cases, _run(split_exe, cases)):
+        total = int((-(-np.asarray(runs) // 256)).sum()) * n_tiles
+        cap = _cap(total, slots)
+        assert b[0] == 0 and b[8] == total and all(x <= y for x, y in zip(b, b[1:]))
+        assert max(y - x for x, y in zip(b, b[1:])) <= cap
+        at, W = _start_of(runs, fw, n_tiles, b[1:8])
+        before, _ = _start_of(runs, fw, n_tiles, [x - 1 for x in b[1:8]])
+        big = max(big, W)
+        for k in range(1, 8):
+            t = -(-k * W // 8)
+            assert before[k - 1] < t <= at[k - 1], (k, b)
+    assert big > 1 << 32
+
+
+def test_floordiv_at_integer_quotients(split_exe):
+    """split_floordiv's float estimate is off by one just below and at exact quotients of large
+    operands; the correction must give floor(a / b) there."""
+    rng = np.random.default_rng(3)
+    pairs = []
+    for _ in range(400):
+        b = int(rng.integers(1, 1 << 42))
+        q = int(rng.integers(0, 1 << 20))
+        for a in (q * b - 1, q * b, q * b + 1, q * b + b - 1):
+            if a >= 0 and a // b < 1 << 20:
+                pairs.append((a, b))
+    text = "".join(f"D {a} {b}\n" for a, b in pairs)
+    out = subprocess.run([str(split_exe)], input=text, capture_output=True, text=True, check=True).stdout.split()
+    assert [int(v) for v in out] == [a // b for a, b in pairs]

@@ -1,0 +1,40 @@
+// Host driver of the packed GEMMs' per-XCD split (cernels_amd/csrc/moe_split.h), for
+// test_xcd_split.py. Reads cases from stdin, one per line:
+//   "S E fw n_tiles slots run_0 .. run_{E-1}" -> the 9 bounds, evaluated the way the route kernel
+//     does: exclusive prefixes of pairs and of 256-row M-tiles over experts, split_expert per
+//     expert, then split_clamp;
+//   "D a b" -> split_floordiv(a, b).
+#include <cstdio>
+#include <vector>
+
+#include "moe_split.h"
+
+int main() {
+    char op;
+    while (std::scanf(" %c", &op) == 1) {
+        if (op == 'D') {
+            long long a, b;
+            if (std::scanf("%lld %lld", &a, &b) != 2) return 1;
+            std::printf("%d\n", cmoe::split_floordiv(a, b));
+            continue;
+        }
+        int E, fw, n_tiles, slots;
+        if (std::scanf("%d %d %d %d", &E, &fw, &n_tiles, &slots) != 4) return 1;
+        std::vector<int> run(E), nt(E), off(E), toff(E);
+        for (auto& r : run) std::scanf("%d", &r);
+        long long tiles = 0, pairs = 0;
+        for (int e = 0; e < E; ++e) {
+            nt[e] = (run[e] + 255) / 256;
+            off[e] = (int)pairs;
+            toff[e] = (int)tiles;
+            tiles += nt[e];
+            pairs += run[e];
+        }
+        int b[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+        for (int e = 0; e < E; ++e)
+            cmoe::split_expert(fw, n_tiles, 256, run[e], nt[e], toff[e], off[e], 32LL * fw * tiles + pairs, b);
+        cmoe::split_clamp(b, (int)tiles * n_tiles, slots);
+        for (int k = 0; k < 9; ++k) std::printf("%d%c", b[k], k == 8 ? '\n' : ' ');
+    }
+    return 0;
+}
