@@ -205,7 +205,8 @@ struct PkParams {
     const int32_t* offsets;        // [E+1]
     const int32_t* tile_offsets;   // [E+1]
     const int32_t* tile_expert;    // [tiles]
-    const int32_t* bounds;         // [9] per-XCD item ranges, written by the route
+    const int32_t* meta;           // [0] = M-tiles
+    const int32_t* bounds;         // [9] per-XCD item ranges written by the route, or null: equal split
     const float* route_w;          // [P] (GEMM2)
     void* out;                     // GEMM1: glu fp16 [P, F]; GEMM2: Y as 24-bit floats [P, H]
     int Kd, NF, KS, n_tiles;
@@ -251,12 +252,20 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
-    const int b_lo = prm.bounds[xcd], b_hi = prm.bounds[xcd + 1];
+    int b_lo, b_hi;
+    if (prm.bounds) {
+        b_lo = prm.bounds[xcd];
+        b_hi = prm.bounds[xcd + 1];
+    } else {
+        const int total = prm.meta[0] * prm.n_tiles, per = ceil_div(total, 8);
+        b_lo = min(xcd * per, total);
+        b_hi = min(b_lo + per, total);
+    }
     const int Kd = prm.Kd, nst = Kd / kBK;
     const int a_chunk = tid & 7;
 
     // Items of XCD x are one contiguous range of the list, [bounds[x], bounds[x+1]) (moe_split.h: of
-    // about equal estimated cost, at most the rounds of an equal split), so that the items that share
+    // about equal estimated cost where workgroups run many items, else equal in count), so that the items that share
     // a weight tile (neighbours in the list) run at about the same time on one XCD's L2. Each slot of
     // the XCD takes offsets s and 2*slots-1-s first (snake order: long and short items mix on every CU), then draws
     // offsets 2*slots + n from the XCD's work counter: workgroups that run faster take more items,
@@ -731,7 +740,7 @@ static int pk_cu_count() {
 
 // Workgroups of a packed GEMM launch: one per CU, a multiple of 8 (the same count on every XCD).
 static int pk_grid(int max_tiles, int n_tiles) {
-    const int grid = min(max_tiles * n_tiles, pk_cu_count());
+    const int grid = (int)std::min<long long>((long long)max_tiles * n_tiles, pk_cu_count());
     return ceil_div(max(grid, 1), 8) * 8;
 }
 
@@ -864,16 +873,22 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
                                  int8_t* psig, hipStream_t s, hipEvent_t* ev) {
     auto mark = [&](int i) { if (ev) (void)hipEventRecord(ev[i], s); };
     // Launch shapes of both GEMMs, from the shape alone; the route then splits each one's items over
-    // the XCDs (meta[32..40] gate_up, meta[41..49] down).
+    // the XCDs (meta[32..40] gate_up, meta[41..49] down). Where even the most M-tiles the route can
+    // make (ceil(P / 256) + min(P, E)) would give each workgroup fewer than 8 rounds of items, the
+    // split is the equal one for both GEMMs (moe_split.h) and the GEMMs compute it themselves.
     const int nf1 = act_is_gated(act) ? F / 16 : F / 32, nf2 = H / 32;
     const int fw1 = pick_fw((long long)T * K, E, nf1, H, pk_cu_count());
     const int fw2 = pick_fw((long long)T * K, E, nf2, F, pk_cu_count());
     const int nt1 = ceil_div(nf1, fw1), nt2 = ceil_div(nf2, fw2);
-    XcdSplit split{{fw1, fw2}, {nt1, nt2}, {pk_grid(max_tiles, nt1) / 8, pk_grid(max_tiles, nt2) / 8}, meta + 32};
+    const int slots1 = pk_grid(max_tiles, nt1) / 8, slots2 = pk_grid(max_tiles, nt2) / 8;
+    const long long P = (long long)T * K, mt_max = (P + kPkBM - 1) / kPkBM + std::min<long long>(P, E);
+    auto max_rounds = [&](int nt, int slots) { return (mt_max * nt + 8LL * slots - 1) / (8LL * slots); };
+    const bool cost_split = max(max_rounds(nt1, slots1), max_rounds(nt2, slots2)) >= 8;
+    XcdSplit split{{fw1, fw2}, {nt1, nt2}, {slots1, slots2}, meta + 32};
     mark(0);
     hipError_t st =
         launch_route(idx, T, K, E, kPkBM, offsets, sorted_pairs, tile_offsets, tile_expert, meta, route_counts,
-                     meta + 8, s, rsig, &split);
+                     meta + 8, s, rsig, cost_split ? &split : nullptr);
     if (st != hipSuccess) return st;
     mark(1);
     PkParams g1{};
@@ -884,7 +899,8 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.offsets = offsets;
     g1.tile_offsets = tile_offsets;
     g1.tile_expert = tile_expert;
-    g1.bounds = meta + 32;
+    g1.meta = meta;
+    g1.bounds = cost_split ? meta + 32 : nullptr;
     g1.route_w = route_w;
     g1.out = glu;
     g1.Kd = H;
@@ -931,7 +947,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.fw = fw2;
     g2.counters = meta + 16;
     g2.n_tiles = nt2;
-    g2.bounds = meta + 41;
+    g2.bounds = cost_split ? meta + 41 : nullptr;
     g2.bias = nullptr;  // the down bias is added by the combine
     st = launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;

@@ -7,11 +7,12 @@
 // reduction over 32 columns (its fw weight fragments of 32 columns and its r activation rows). Expert
 // e's items cost n_tiles * (32 fw nt_e + run_e) together, so the cost before expert e is
 // n_tiles * (32 fw toff_e + off_e), from the two prefixes the route has already scanned. XCD x starts
-// at the first item whose cost prefix reaches ceil(x W / 8) of the total W. Then no range may hold more
-// than cap items: the rounds of items an equal split gives each workgroup,
-// r = ceil(ceil(items / 8) / slots), plus r / 8. Where rounds are few, one more item in a workgroup
-// costs a whole round, more than the balance gains; where they are many, the extra items are the
-// cheap ones.
+// at the first item whose cost prefix reaches ceil(x W / 8) of the total W. The split applies where an
+// equal split of the items gives each workgroup r = ceil(ceil(items / 8) / slots) >= 8 rounds of
+// items, and no range may then hold more than (r + r / 8) * slots items. With fewer rounds the equal
+// split stays: there one more item in a workgroup costs a whole round, and the XCD's end is set by how
+// its items fall into rounds rather than by their summed cost (measured: at 4 rounds the cost split
+// was 1-3% slower, at 8-10 rounds 3.5% faster).
 #pragma once
 
 #ifndef CMOE_HD
@@ -48,10 +49,15 @@ CMOE_HD inline void split_expert(int fw, int n_tiles, int bm, int run, int nt, i
     }
 }
 
-// b[1..7] from split_expert (0 where no expert wrote one: the list is empty) -> final bounds b[0..8].
+// b[1..7] from split_expert -> final bounds b[0..8]: the equal split below 8 rounds, else b clamped
+// to at most cap items per range. Any b[1..7] gives a valid split (an empty list gives all zeros).
 CMOE_HD inline void split_clamp(int* b, int total, int slots) {
-    const int rounds = ((total + 7) / 8 + slots - 1) / slots, cap = (rounds + rounds / 8) * slots;
+    const int per = (total + 7) / 8, rounds = (per + slots - 1) / slots, cap = (rounds + rounds / 8) * slots;
     b[0] = 0;
+    if (rounds < 8) {
+        for (int k = 1; k < 9; ++k) b[k] = k * per < total ? k * per : total;
+        return;
+    }
     for (int k = 1; k < 8; ++k) {
         int v = b[k];
         v = v < b[k - 1] + cap ? v : b[k - 1] + cap;

@@ -144,6 +144,21 @@ def test_packed_small(device, case):
     assert_reference_verify(out, oracle_eager(c), str(case))
 
 
+def test_packed_cost_split_many_rounds(device):
+    """2048 tokens x 8 of 16 experts with skewed routing, F = 4096: ~2200 items, so each of the 256
+    workgroups runs 8+ rounds and the route writes cost-balanced per-XCD item ranges, over M-tiles of
+    many sizes. A sample of 160 tokens is checked against the fp64 oracle and the reference's
+    op_eager bar."""
+    c = rand_case(31, 2048, 128, 4096, 16, 8, skew=1.5)
+    runs = torch.bincount(c["idx"].flatten(), minlength=16)
+    assert int((-(-runs // 256)).sum()) * 32 >= 8 * 8 * 32  # >= 8 rounds at fw = 8 on 256 CUs
+    print("[packed cost split] T2048 H128 F4096 E16 k8", flush=True)
+    out = _run_packed(c, device).cpu()
+    rows = torch.randperm(2048, generator=torch.Generator().manual_seed(5))[:160]
+    assert_within_tolerance(out[rows], oracle_fp64(c, rows), "cost split")
+    assert_reference_verify(out[rows], oracle_eager(c, rows), "cost split")
+
+
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
 def test_packed_golden(device, name):
     t, meta = load_golden(name)

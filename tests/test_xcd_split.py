@@ -3,9 +3,10 @@
 The route kernel computes them in integer and float arithmetic per expert; here the same header is
 compiled for the host and its bounds are compared with the definition counted item by item: XCD x
 starts at the first item whose cost prefix reaches ceil(x W / 8), an item of r rows costing
-32 fw + r. Where that split would give some XCD more than cap items (the R rounds an equal
-split gives each workgroup, plus R / 8) the bounds are clamped; every result covers the list once, in
-order, with at most cap items per XCD.
+32 fw + r, where an equal split of the items gives each workgroup R >= 8 rounds; with fewer rounds
+the split is the equal one. Where the cost split would give some XCD more than cap items (R rounds
+plus R / 8) the bounds are clamped; every result covers the list once, in order, with at most cap
+items per XCD.
 """
 
 from __future__ import annotations
@@ -46,8 +47,12 @@ def _by_definition(runs, fw, n_tiles):
     return [int(np.searchsorted(start, -(-k * W // 8), side="left")) for k in range(9)], len(costs)
 
 
+def _rounds(total, slots):
+    return -(-(-(-total // 8)) // slots)
+
+
 def _cap(total, slots):
-    rounds = -(-(-(-total // 8)) // slots)
+    rounds = _rounds(total, slots)
     return (rounds + rounds // 8) * slots
 
 
@@ -82,23 +87,28 @@ def test_split_matches_the_item_count_definition(split_exe):
     cases = _cases()
     got = _run(split_exe, cases)
     assert len(got) == len(cases)
-    clamped = 0
+    equal = split = clamped = 0
     for (runs, fw, n_tiles, slots), b in zip(cases, got):
         want, total = _by_definition(runs, fw, n_tiles)
         cap = _cap(total, slots)
         assert b[0] == 0 and b[8] == total and all(x <= y for x, y in zip(b, b[1:])), (runs[:8], b)
         assert max(y - x for x, y in zip(b, b[1:])) <= cap, (b, cap)
-        if max(y - x for x, y in zip(want, want[1:])) <= cap:
+        if _rounds(total, slots) < 8:
+            per = -(-total // 8)
+            assert b == [min(k * per, total) for k in range(9)]
+            equal += 1
+        elif max(y - x for x, y in zip(want, want[1:])) <= cap:
             assert b == want, (fw, n_tiles, slots, b, want)
+            split += 1
         else:
             clamped += 1
-    assert clamped > 0  # the clamp is exercised too
+    assert min(equal, split, clamped) > 0  # every branch is exercised
 
 
 def test_equal_items_split_evenly(split_exe):
-    """Experts of equal size: the cost split is the equal item split."""
-    (b,) = _run(split_exe, [([256] * 64, 8, 8, 32)])
-    assert b == [64 * x for x in range(9)]
+    """Experts of equal size: the cost split is the equal item split (16 rounds of 8 workgroups)."""
+    (b,) = _run(split_exe, [([256] * 64, 8, 16, 8)])
+    assert b == [128 * x for x in range(9)]
 
 
 def test_split_of_long_lists(split_exe):
