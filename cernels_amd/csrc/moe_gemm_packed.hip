@@ -763,9 +763,10 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
                         const XcdSplit* split = nullptr);
 // out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] * 2^psig + w[t, k] * b2[e] ), slots in k
 // order, Y in the 24-bit float form the packed down GEMM writes (w * glu W2, without the bias; psig only
-// when some glu row was stored scaled). One workgroup per token; a thread owns 8 consecutive columns
-// (two 12-byte loads per slot).
-__global__ __launch_bounds__(256) void moe_combine_h_kernel(const unsigned char* __restrict__ Yb,
+// when some glu row was stored scaled). One workgroup per token, H/8 threads rounded up to whole waves;
+// a thread owns 8 consecutive columns (two 12-byte loads per slot) and issues the loads of four slots
+// before it adds them, still in slot order.
+__global__ __launch_bounds__(1024) void moe_combine_h_kernel(const unsigned char* __restrict__ Yb,
                                                             const int32_t* __restrict__ idx, uint16_t* __restrict__ out,
                                                             int T, int K, int E, int H,
                                                             const int32_t* __restrict__ sync,
@@ -775,27 +776,38 @@ __global__ __launch_bounds__(256) void moe_combine_h_kernel(const unsigned char*
     const bool scaled = sync[1] != 0;  // some glu row was stored scaled: its Y row is scaled by 2^-psig
     for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
         f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < K; ++k) {
-            const int e = idx[t * K + k];
-            if ((unsigned)e >= (unsigned)E) continue;
-            const unsigned char* src = Yb + (((long long)t * K + k) * H + 8 * c) * 3;
-            f24x4 q0, q1;
-            __builtin_memcpy(&q0, src, 12);
-            __builtin_memcpy(&q1, src + 12, 12);
-            f32x4 y0 = unpack_f24x4(q0), y1 = unpack_f24x4(q1);
-            if (scaled) {
-                const float sc = __builtin_amdgcn_ldexpf(1.0f, psig[(long long)t * K + k]);
-                y0 *= sc;
-                y1 *= sc;
+        for (int k0 = 0; k0 < K; k0 += 4) {
+            f24x4 q[4][2];
+            int ev[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = k0 + j;
+                ev[j] = k < K ? idx[t * K + k] : -1;
+                if ((unsigned)ev[j] < (unsigned)E) {
+                    const unsigned char* src = Yb + (((long long)t * K + k) * H + 8 * c) * 3;
+                    __builtin_memcpy(&q[j][0], src, 12);
+                    __builtin_memcpy(&q[j][1], src + 12, 12);
+                }
             }
-            if (bias) {  // the slot's share of the down bias, w * b[e]
-                const float w = route_w[(long long)t * K + k];
-                const f32x4* b = reinterpret_cast<const f32x4*>(bias + (long long)e * H + 8 * c);
-                y0 += w * b[0];
-                y1 += w * b[1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = k0 + j, e = ev[j];
+                if ((unsigned)e >= (unsigned)E) continue;
+                f32x4 y0 = unpack_f24x4(q[j][0]), y1 = unpack_f24x4(q[j][1]);
+                if (scaled) {
+                    const float sc = __builtin_amdgcn_ldexpf(1.0f, psig[(long long)t * K + k]);
+                    y0 *= sc;
+                    y1 *= sc;
+                }
+                if (bias) {  // the slot's share of the down bias, w * b[e]
+                    const float w = route_w[(long long)t * K + k];
+                    const f32x4* bb = reinterpret_cast<const f32x4*>(bias + (long long)e * H + 8 * c);
+                    y0 += w * bb[0];
+                    y1 += w * bb[1];
+                }
+                s0 += y0;
+                s1 += y1;
             }
-            s0 += y0;
-            s1 += y1;
         }
         *reinterpret_cast<u32x4*>(out + (long long)t * H + 8 * c) =
             u32x4{pack_bf16x2(s0[0], s0[1]), pack_bf16x2(s0[2], s0[3]), pack_bf16x2(s1[0], s1[1]), pack_bf16x2(s1[2], s1[3])};
@@ -952,8 +964,9 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     st = launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(3);
-    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(256), 0, s, reinterpret_cast<const unsigned char*>(Y), idx,
-                       static_cast<uint16_t*>(out), T, K, E, H, meta + 24, psig, b2, route_w);
+    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(std::min(1024, ceil_div(H / 8, kWave) * kWave)), 0, s,
+                       reinterpret_cast<const unsigned char*>(Y), idx, static_cast<uint16_t*>(out), T, K, E, H, meta + 24,
+                       psig, b2, route_w);
     st = hipGetLastError();
     mark(4);
     return st;
