@@ -582,11 +582,13 @@ def main():
                     help="run the reference's benchmark runner on its own config names (comma list or 'all'): "
                          "op_eager = the transformers module, custom = the drop-in loader; one JSON record each")
     ap.add_argument("--inner-traffic", metavar="WORKLOAD", help=argparse.SUPPRESS)
-    ap.add_argument("--report", default=str(ROOT / "gpurun_out" / "bench_report.json"))
+    ap.add_argument("--report", metavar="PATH", help="also write the full per-workload record (JSON) to PATH")
+    ap.add_argument("--analysis-root", default="analysis",
+                    help="--reference-configs: where the runner's <host>/<config>.{json,log} records go")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures the experts op on one GPU "
-              f"(the multi-GPU design is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(collectives and sharding are design-only here); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.inner_traffic:
         _inner_traffic(args.inner_traffic)
@@ -608,7 +610,7 @@ def main():
     hip = _hip()
     if args.reference_configs:
         names = REFERENCE_CONFIGS if args.reference_configs == "all" else args.reference_configs.split(",")
-        recs = {n: run_reference_config(n, ROOT / "gpurun_out" / "analysis") for n in names}
+        recs = {n: run_reference_config(n, Path(args.analysis_root)) for n in names}
         print(json.dumps({"metric": "reference configs: custom vs op_eager (transformers module), ms per call",
                           "unit": "ms", "higher_is_better": False, "n_gpus": 1, "configs": recs}), flush=True)
         return
@@ -690,12 +692,10 @@ def main():
         "module_ops": {n: {k: (round(v, 5) if isinstance(v, float) else v) for k, v in r.items()} for n, r in mods.items()},
         "calibration": calibration,
     }
-    try:
+    if args.report:
         Path(args.report).parent.mkdir(parents=True, exist_ok=True)
         Path(args.report).write_text(json.dumps({"line": line, "per_config_full": per, "traffic": traffic}, indent=1,
                                                 default=float))
-    except OSError:
-        pass
     print(json.dumps(line), flush=True)
 
 
