@@ -159,6 +159,19 @@ def test_packed_cost_split_many_rounds(device):
     assert_reference_verify(out[rows], oracle_eager(c, rows), "cost split")
 
 
+@pytest.mark.parametrize("T", [3200, 4096], ids=["count_scan_route", "two_launch_route"])
+def test_packed_cost_split_other_route_kernels(device, T):
+    """The same per-XCD split written by the route's other two kernels: E = 1024 experts with
+    T x 8 pairs is past the one-launch route's LDS (count + scan in one launch at 25 route tiles,
+    separate launches at 32), and ~4000 small items give every workgroup 8+ rounds."""
+    c = rand_case(41, T, 64, 512, 1024, 8, skew=1.0)
+    print(f"[packed cost split, route T={T}] H64 F512 E1024 k8", flush=True)
+    out = _run_packed(c, device).cpu()
+    rows = torch.randperm(T, generator=torch.Generator().manual_seed(6))[:256]
+    assert_within_tolerance(out[rows], oracle_fp64(c, rows), f"cost split route T={T}")
+    assert_reference_verify(out[rows], oracle_eager(c, rows), f"cost split route T={T}")
+
+
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
 def test_packed_golden(device, name):
     t, meta = load_golden(name)
