@@ -91,12 +91,14 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 }
 
 // 24-bit floats: the top 24 bits of the fp32 pattern (sign, 8-bit exponent, 15-bit mantissa), rounded
-// to nearest even on the 8 dropped bits (2^-16 relative rounding, fp32's range). inf stays inf and
-// nan stays nan. Four of them pack into three dwords, value i in bytes 3i..3i+2.
+// to nearest even on the 8 dropped bits (2^-16 relative rounding, fp32's range; values past the largest
+// 24-bit float round to inf). inf stays inf; a nan becomes the quiet nan (its rounding could carry it
+// into inf). Branch-free: five VALU instructions per value. Four of them pack into three dwords, value
+// i in bytes 3i..3i+2.
 __device__ __forceinline__ uint32_t f32_to_f24(float f) {
     const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7f800000u) == 0x7f800000u) return (u >> 8) | ((u & 0xffu) ? 1u : 0u);
-    return (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
+    const uint32_t r = (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
+    return __builtin_isnan(f) ? 0x7fc000u : r;
 }
 __device__ __forceinline__ float f24_to_f32(uint32_t r) { return __uint_as_float(r << 8); }
 struct f24x4 {

@@ -690,16 +690,13 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     if (mb >= nmb) break;
                     const int row = mb * 32 + (lane & 31);
                     if (row < rows) {
-                        const float w = s_w[tb][row];
+                        const float ws = wsc * s_w[tb][row];  // exact: wsc is a power of two
                         const long long p = s_pair[tb][row];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             float a[4];
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj) {
-                                const float v = acc[mb][4 * i + jj] * wsc;
-                                a[jj] = v * w;
-                            }
+                            for (int jj = 0; jj < 4; ++jj) a[jj] = acc[mb][4 * i + jj] * ws;
                             const f24x4 q = pack_f24x4(a[0], a[1], a[2], a[3]);
                             __builtin_memcpy(Yb + (p * prm.H + 32 * fc + 8 * i + c4) * 3, &q, 12);
                         }
