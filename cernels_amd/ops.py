@@ -223,6 +223,12 @@ def moe_experts_packed(x: torch.Tensor, packed: PackedExperts, indices: torch.Te
         _require(b is None or (b.dtype == torch.float32 and tuple(b.shape) == (packed.E, n)),
                  "biases must be float32 [E, 2F] and [E, H]")
     L = _native.lib()
+    # the kernels read packed_weight_bytes(H, F, E) of each buffer: a buffer packed for other sizes is refused
+    gu_which = _native.GATE_UP if packed.act in (ACT_SILU, ACT_GPTOSS) else _native.UP  # non-gated: w1 as UP
+    for t, which, name in ((packed.gate_up, gu_which, "packed gate_up"), (packed.down, _native.DOWN, "packed down")):
+        need = L.cernels_moe_packed_weight_bytes(packed.H, packed.F, packed.E, which)
+        _require(need > 0 and t.dtype == torch.uint8 and t.numel() == need,
+                 f"{name} must be the uint8 buffer pack_weights makes for H={packed.H} F={packed.F} E={packed.E}")
     if out is None:
         out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     else:

@@ -74,6 +74,14 @@ def test_packed_entry_checks_every_argument(device):
     host_pk = ops.PackedExperts(pk.gate_up.cpu(), pk.down, pk.H, pk.F, pk.E, pk.act, pk.bias_layout)
     with pytest.raises(RuntimeError, match="packed gate_up"):
         ops.moe_experts_packed(x, host_pk, idx, w, K)
+    for what, kw in {"gate_up packed for fewer experts": dict(gate_up=pk.gate_up[: pk.gate_up.numel() // 2]),
+                     "down packed for fewer experts": dict(down=pk.down[: pk.down.numel() // 2]),
+                     "more experts than packed": dict(E=E + 1)}.items():
+        f = dict(gate_up=pk.gate_up, down=pk.down, E=pk.E) | kw
+        short_pk = ops.PackedExperts(f["gate_up"], f["down"], pk.H, pk.F, f["E"], pk.act, pk.bias_layout)
+        with pytest.raises(RuntimeError, match="packed"):
+            ops.moe_experts_packed(x, short_pk, idx, w, K)
+        print(f"[checks] rejected: {what}", flush=True)
     bias_pk = ops.PackedExperts(pk.gate_up, pk.down, pk.H, pk.F, pk.E, pk.act, pk.bias_layout,
                                 gate_up_bias=torch.zeros(E, 2 * F, device=device, dtype=torch.bfloat16))
     with pytest.raises(RuntimeError, match="biases"):
