@@ -498,8 +498,10 @@ def run_reference_config(name, out_dir):
 
     from cernels_amd.benchmark import main as runner
 
-    results = runner.main(name, root=out_dir)
-    return {w: asdict(r) for w, r in results.items()}
+    outcome = runner.main(name, root=out_dir)
+    rec = {w: asdict(r) for w, r in outcome.results.items()}
+    rec.update({w: {"skipped": why} for w, why in outcome.skipped.items()})
+    return rec
 
 
 # ---- HBM traffic per launch (rocprofv3 counters, child processes) ----------------------------------

@@ -45,7 +45,7 @@ def library_sha() -> str:
     return h.hexdigest()[:12]
 
 
-def record(name, cfg, results, ref_label) -> dict:
+def record(name, cfg, results, ref_label, skipped=None) -> dict:
     declared = {
         "op_eager": cfg.baseline is not None and not cfg.reference_is_hub,
         "op_compile": cfg.baseline is not None and not cfg.reference_is_hub and cfg.use_compile,
@@ -64,11 +64,12 @@ def record(name, cfg, results, ref_label) -> dict:
         "declared": declared,
         "provenance": {"repo": None, "version": None, "kernel_commit_sha": None, "custom_sha": library_sha()},
         "workloads": {w: asdict(t) if is_dataclass(t) else dict(t) for w, t in results.items()},
+        "skipped": dict(skipped or {}),  # declared workloads that raised, with the reason
     }
 
 
-def save(name, cfg, results, log, ref_label="op_eager", root=ANALYSIS) -> Path:
-    rec = record(name, cfg, results, ref_label)
+def save(name, cfg, results, log, ref_label="op_eager", root=ANALYSIS, skipped=None) -> Path:
+    rec = record(name, cfg, results, ref_label, skipped)
     out = Path(root) / rec["machine"]["host"]
     out.mkdir(parents=True, exist_ok=True)
     path = out / f"{name}.json"

@@ -4,7 +4,8 @@ Usage: python -m cernels_amd.benchmark.view [--root DIR]   (default root: analys
 
 Columns: each workload's mean ms; each contender's speedup over the reference bar (op_compile if it
 ran, else op_eager, else hub); each contender's verdict: "ok" (verified), "FAIL" (verify failed),
-"." (ran without a verdict, or declared but did not run), "-" (the config has no such workload).
+"." (ran without a verdict, or declared but did not run), "-" (the config has no such workload). A
+declared workload that raised shows "skip" in its ms column (the reason is in the record).
 """
 
 from __future__ import annotations
@@ -43,8 +44,9 @@ def rows(records) -> list[list[str]]:
         ver = ["-" if w == ref else _mark(declared.get(w, False), w in mean, r["workloads"].get(w, {}).get("verified"))
                for w in CONTENDERS]
         mach = r["machine"]
-        out.append([r["config"], str(mach.get("gpu")), str(mach.get("gcn_arch") or mach.get("arch")),
-                    *(f"{mean[w]:.3f}" if w in mean else "-" for w in WORKLOADS), *vs, *ver])
+        skipped = r.get("skipped", {})
+        ms = [f"{mean[w]:.3f}" if w in mean else ("skip" if w in skipped else "-") for w in WORKLOADS]
+        out.append([r["config"], str(mach.get("gpu")), str(mach.get("gcn_arch") or mach.get("arch")), *ms, *vs, *ver])
     return out
 
 

@@ -6,11 +6,13 @@ eagerly, "op_eager"), ``custom(*inputs)`` (the drop-in loader), ``hub`` / ``lib`
 none here), ``reference_is_hub`` (the baseline is itself a Hub kernel) and ``use_compile`` (also time
 ``torch.compile(baseline)`` as "op_compile"), and ``verify(out, ref)``.
 
-``use_compile`` is off for every config here: the transformers experts loop is data dependent
-(``nonzero`` / ``where`` per hit expert), so compiling it breaks the graph at every expert, and the
-reference's own published op_compile times equal its op_eager times within 10%. A config whose
-baseline is unavailable offline (the megablocks Hub kernel) has ``baseline = None``; the runner then
-times ``custom`` alone.
+``use_compile`` is on, as in the reference's MoE configs (src/configs/registry/cohere2_moe_experts.py:30,
+deepseek_ocr2_moe_experts.py:33, gpt_oss_moe_experts.py:27, qwen3_next_moe_experts.py:39). The
+transformers experts loop is data dependent (``nonzero`` / ``where`` per hit expert), so the compiled
+baseline runs as many small graphs with breaks between them; where compiling fails the runner records
+op_compile as skipped, with the reason. A config whose baseline is unavailable offline (the megablocks
+Hub kernel) has ``baseline = None`` and ``use_compile`` off (src/configs/registry/megablocks_moe.py:21-22);
+the runner then times ``custom`` alone.
 """
 
 from __future__ import annotations
@@ -33,7 +35,7 @@ class Config:
     hub: Callable[..., Any] | None = None
     lib: Callable[..., Any] | None = None
     reference_is_hub: bool = False
-    use_compile: bool = False
+    use_compile: bool = True
 
     def inputs(self, device, dtype=torch.bfloat16) -> tuple:
         raise NotImplementedError

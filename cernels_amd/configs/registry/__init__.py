@@ -225,6 +225,7 @@ class MegablocksConfig(Config):
 
     gated = False
     reference_is_hub = True  # the reference's baseline is the Hub kernel, which needs the network
+    use_compile = False
 
     def __init__(self):
         self.name = "megablocks_moe"

@@ -48,7 +48,8 @@ def test_saved_record_and_table(tmp_path):
     rec = json.loads(path.read_text())
     assert path.parent.parent == tmp_path and path.with_suffix(".log").read_text() == "log text\n"
     assert rec["config"] == "cohere2_moe_experts" and rec["reference"] == "op_eager" and rec["dtype"] == "bfloat16"
-    assert rec["declared"] == {"op_eager": True, "op_compile": False, "hub": False, "lib": False, "custom": True}
+    assert rec["declared"] == {"op_eager": True, "op_compile": True, "hub": False, "lib": False, "custom": True}
+    assert rec["skipped"] == {}
     s = cfg.shape
     assert rec["input_shapes"] == [[s.tokens, s.hidden], [s.tokens, s.top_k], [s.tokens, s.top_k]]
     assert len(rec["provenance"]["custom_sha"]) == 12
@@ -63,13 +64,61 @@ def test_saved_record_and_table(tmp_path):
     assert "no results" in view.main(tmp_path / "empty")
 
 
-def test_megablocks_reference_is_the_absent_hub_kernel():
+def test_lineup_follows_the_protocol_order():
     from cernels_amd.configs.registry import CONFIGS
 
-    wl, ref = runner.workloads(CONFIGS["megablocks_moe"])
-    assert ref is None and list(wl) == ["custom"]
-    wl, ref = runner.workloads(CONFIGS["qwen3_next_moe_experts"])
-    assert ref == "op_eager" and list(wl) == ["op_eager", "custom"]
+    assert [e.label for e in runner.lineup(CONFIGS["megablocks_moe"])] == ["custom"]  # its reference is offline
+    for name in ("cohere2_moe_experts", "deepseek_ocr2_moe_experts_decode", "gpt_oss_moe_experts", "qwen3_next_moe_experts"):
+        ent = runner.lineup(CONFIGS[name])
+        assert [e.label for e in ent] == ["op_eager", "op_compile", "custom"], name
+        assert [e.is_reference for e in ent] == [True, False, False]
+
+
+def _small_experts_config():
+    from cernels_amd.configs.registry import ExpertsConfig
+    from cernels_amd.configs.synth import MoeShape
+
+    cfg = ExpertsConfig(MoeShape("cohere2_small", tokens=9, hidden=64, ffn=32, experts=8, top_k=2))
+    cfg.custom = cfg.baseline  # a contender that is the reference itself: verifies, speedup about 1
+    return cfg
+
+
+def test_run_records_each_workload_and_the_skips(monkeypatch, tmp_path):
+    """On the CPU with a stand-in compile: the reference is measured first, contenders are verified
+    against its output and get a speedup; a workload that raises is recorded under ``skipped`` (in the
+    outcome and the saved record) and the run goes on."""
+    cfg = _small_experts_config()
+
+    def broken_compile(c):
+        def call(*args):
+            raise RuntimeError("compile failed on purpose\nsecond line")
+        return call
+
+    monkeypatch.setattr(runner, "_compiled_baseline", broken_compile)
+    out = runner.run(cfg, device="cpu", warmup=1, budget_s=0.02)
+    assert out.reference == "op_eager" and list(out.results) == ["op_eager", "custom"]
+    assert out.skipped == {"op_compile": "RuntimeError: compile failed on purpose"}
+    assert out.results["op_eager"].verified is None and out.results["op_eager"].speedup is None
+    assert out.results["custom"].verified is True and out.results["custom"].speedup > 0
+    path = save.save(cfg.name, cfg, out.results, "log\n", ref_label=out.reference, root=tmp_path, skipped=out.skipped)
+    rec = json.loads(path.read_text())
+    assert rec["skipped"] == out.skipped and set(rec["workloads"]) == {"op_eager", "custom"}
+    table = view.rows(view.load(tmp_path))
+    assert table[1][table[0].index("op_compile ms")] == "skip"
+    assert "skipped" in runner.table(out)
+
+    only = runner.run(cfg, device="cpu", warmup=1, budget_s=0.02, only=("custom",))
+    assert list(only.results) == ["custom"] and only.results["custom"].verified is True
+
+
+def test_op_compile_is_torch_compile_of_the_baseline():
+    """The real op_compile entrant on the CPU (inductor's C++ backend): the compiled transformers experts
+    forward equals op_eager bit for bit on a small shape."""
+    cfg = _small_experts_config()
+    cfg.custom = None
+    out = runner.run(cfg, device="cpu", warmup=1, budget_s=0.02)
+    assert out.skipped == {} and list(out.results) == ["op_eager", "op_compile"]
+    assert out.results["op_compile"].verified is True
 
 
 @pytest.mark.parametrize("layout", ["concat", "deepseek", "interleaved"])
@@ -99,8 +148,9 @@ def test_op_eager_baseline_is_the_transformers_forward(layout):
 @pytest.mark.gpu
 def test_reference_config_end_to_end(device, tmp_path):
     print("[benchmark runner] cohere2_moe_experts_decode", flush=True)
-    results = runner.main("cohere2_moe_experts_decode", root=tmp_path)
-    assert set(results) == {"op_eager", "custom"}
+    out = runner.main("cohere2_moe_experts_decode", root=tmp_path, only=("op_eager", "custom"))
+    results = out.results
+    assert set(results) == {"op_eager", "custom"} and out.skipped == {}
     assert results["custom"].verified is True and results["custom"].speedup > 1.0
     rec = json.loads(next(tmp_path.glob("*/cohere2_moe_experts_decode.json")).read_text())
     assert rec["machine"]["gcn_arch"].startswith("gfx950")
