@@ -71,7 +71,7 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     w.sorted_pairs = o; o = align_up(o + sizeof(int32_t) * P);
     w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
     w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));
-    w.glu = o;          o = align_up(o + sizeof(uint16_t) * P * F);
+    w.glu = o;          o = align_up(o + sizeof(uint16_t) * 2 * P * F);  // stored layout: bf16 pairs; packed: fp16
     w.Y = o;            o = align_up(o + sizeof(float) * P * H);  // fp32 (stored layout) or 24-bit floats (packed)
     w.gexp = o;         o = align_up(o + (size_t)P * (F / 16));  // packed path: exponent per 16-column glu segment
     w.rsig = o;         o = align_up(o + (size_t)P);             // packed path: per glu row scale
@@ -330,16 +330,26 @@ size_t cernels_moe_experts_decode_workspace_bytes(int32_t T, int32_t H, int32_t 
     return decode_ws(T, H, F, K).total;
 }
 
+namespace {
+// Every check of the decode entry except the workspace's size, in the entry's order.
+int decode_checks(const void* x, const void* w1, const void* w2, const int32_t* idx, const float* wts, int T, int H,
+                  int F, int E, int K, int layout, int act, void* out, const void* ws) {
+    int st = common_checks(x, w1, w2, idx, wts, T, H, F, E, K, layout, act, out, const_cast<void*>(ws));
+    if (st != CERNELS_MOE_OK || T == 0) return st;
+    if (layout != CERNELS_MOE_LAYOUT_CONCAT || !act_gated(act)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (T > cmoe::decode_max_tokens() || T * K > cmoe::decode_max_pairs()) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (H % 8 || F % 8 || !cmoe::decode_shape_supported(H, F)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    return CERNELS_MOE_OK;
+}
+}  // namespace
+
 int cernels_moe_experts_decode_staged(const void* x, const void* gate_up_proj, const float* gate_up_bias,
                                       const void* down_proj, const float* down_bias, const int32_t* indices,
                                       const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
                                       int32_t layout, int32_t act, void* out, void* workspace,
                                       size_t workspace_bytes, hipStream_t stream, hipEvent_t* stage_events) {
-    int st = common_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
+    int st = decode_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out, workspace);
     if (st != CERNELS_MOE_OK || T == 0) return st;
-    if (layout != CERNELS_MOE_LAYOUT_CONCAT || !act_gated(act)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
-    if (T > cmoe::decode_max_tokens() || T * K > cmoe::decode_max_pairs()) return CERNELS_MOE_UNSUPPORTED_SHAPE;
-    if (H % 8 || F % 8 || !cmoe::decode_shape_supported(H, F)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     const DecodeWs w = decode_ws(T, H, F, K);
     if (workspace_bytes < w.total) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
     char* base = static_cast<char*>(workspace);
@@ -365,10 +375,13 @@ int cernels_moe_experts_decode_noalloc(const void* x, const void* gate_up_proj, 
                                        const void* down_proj, const float* down_bias, const int32_t* indices,
                                        const float* weights, int32_t T, int32_t H, int32_t F, int32_t E, int32_t K,
                                        int32_t layout, int32_t act, void* out, hipStream_t stream) {
-    // The library's static per-GPU scratch takes the place of the workspace; every check of the decode
-    // entry applies (a shape it accepts always fits the scratch; the size check stays as a guard).
-    if (!dims_ok(T, H, F, E, K)) return CERNELS_MOE_INVALID_ARGUMENT;
-    if (T == 0) return CERNELS_MOE_OK;
+    // The library's static per-GPU scratch takes the place of the workspace. Every check of the decode
+    // entry runs first, in its order, so a call is refused exactly as the decode entry refuses it (a
+    // shape it accepts always fits the scratch; the size check after them stays as a guard).
+    alignas(16) static const unsigned char kStandIn[16] = {};  // the scratch in the pointer checks
+    const int st = decode_checks(x, gate_up_proj, down_proj, indices, weights, T, H, F, E, K, layout, act, out,
+                                 kStandIn);
+    if (st != CERNELS_MOE_OK || T == 0) return st;
     if (decode_ws(T, H, F, K).total > cmoe::decode_noalloc_bytes()) return CERNELS_MOE_WORKSPACE_TOO_SMALL;
     void* ws = nullptr;
     if (cmoe::decode_noalloc_scratch(&ws) != hipSuccess) return CERNELS_MOE_HIP_ERROR;

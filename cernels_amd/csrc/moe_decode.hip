@@ -16,6 +16,7 @@
 #include <mutex>
 
 #include "moe_common.h"
+#include "../../include/cernels_moe.h"
 
 namespace cmoe {
 
@@ -466,6 +467,8 @@ hipError_t launch_decode(const uint16_t* x, const uint16_t* w1, const float* b1,
 // The decode kernels write every byte they read from it, so nothing needs clearing between calls;
 // calls that overlap on one GPU share it and race.
 constexpr size_t kDecNoAllocBytes = (size_t)kDecMaxPairs * 4096 * 2 + (size_t)kDecMaxPairs * 4;
+static_assert(kDecNoAllocBytes == CERNELS_MOE_DECODE_NOALLOC_SCRATCH_BYTES,
+              "the public header states the scratch size");
 static __device__ __align__(256) unsigned char scratch[kDecNoAllocBytes];
 
 size_t decode_noalloc_bytes() { return kDecNoAllocBytes; }

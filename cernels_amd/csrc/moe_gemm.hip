@@ -6,6 +6,16 @@
 // Y stays fp32: rounding each of the K weighted rows to bf16 before the k-sum costs about
 // 0.006*RMS of extra error, more than the 2e-2*RMS budget leaves after the output's own rounding.
 //
+// glu as a bf16 pair. GEMM1 stores each glu value v as hi = bf16(v) and lo = bf16(v - hi); hi + lo
+// carries v to about 2^-17 relative, where one bf16 rounding (2^-9) costs up to 0.008*RMS of output
+// error (0.0207 / 0.0226 / 0.0262 against the 2e-2*RMS bar on the deepseek-v2-lite, 30B-A3B and
+// qwen3-next Zipf workloads, by a float64 simulation of that rounding alone; with the pair the error
+// is the output's own bf16 rounding, 0.0127 / 0.0189 / 0.0183). A glu row is 2F bf16 values: per
+// 64 columns, the 64 hi values then the 64 lo values. GEMM2 reduces over those 2F values: stage s
+// reads A columns [64s, 64s + 64) and the weights of k-chunk s / 2 (b_kshift = 1), so every weight
+// chunk meets its glu twice, once as hi and once as lo. This doubles GEMM2's MFMAs and its weight
+// reads from L2; the weights still come from HBM once per tile.
+//
 // Replaces the reference's per-expert host loop (src/kops/cohere2_moe_experts/csrc/
 // cohere2_moe_experts.cu:315-358: gather_kernel, cublasGemmEx x2, swiglu_kernel,
 // scatter_add_f32_kernel, final cast; gpt-oss adds add_gateup_bias_kernel,
@@ -38,7 +48,7 @@ constexpr int kModeGateUp = 0;
 constexpr int kModeDown = 1;
 
 struct GemmParams {
-    const uint16_t* A;             // GEMM1: x [T, H]; GEMM2: glu [P, F] (rows in expert order)
+    const uint16_t* A;             // GEMM1: x [T, H]; GEMM2: glu pairs [P, 2F] (rows in expert order)
     const uint16_t* B;             // expert weights, expert 0
     const float* bias;             // GEMM1: [E, 2F]; GEMM2: [E, H]; or null
     const int32_t* sorted_pairs;   // [P] pair id per expert-ordered row
@@ -47,15 +57,26 @@ struct GemmParams {
     const int32_t* tile_expert;    // [tiles]
     const int32_t* meta;           // [0] = tiles
     const float* route_w;          // [P] fp32 routing weight per pair (GEMM2)
-    void* out;                     // GEMM1: glu bf16 [P, F]; GEMM2: Y fp32 [P, H]
-    int Kdim;                      // reduction length: H (GEMM1) or F (GEMM2)
+    void* out;                     // GEMM1: glu pairs bf16 [P, 2F]; GEMM2: Y fp32 [P, H]
+    int Kdim;                      // A's row length and the stages' span: H (GEMM1) or 2F (GEMM2)
     int N;                         // output columns: F (GEMM1) or H (GEMM2)
     int F;                         // expert intermediate size
     int topk;
     int n_tiles;                   // output column tiles
     long long expert_stride;       // elements of one expert's matrix in B
     int ldb;                       // row stride of B (elements)
+    int b_kshift;                  // B's k-chunk of stage s is s >> b_kshift (GEMM2 reads the glu pair: 1)
 };
+
+// glu value v as the bf16 pair (hi, lo): hi = bf16(v), lo = bf16(v - hi) (lo = 0 where v is not finite).
+__device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) {
+    hi = f32_to_bf16_bits(v);
+    const float r = v - bf16_bits_to_f32(hi);
+    lo = f32_to_bf16_bits(r == r && fabsf(r) != __builtin_inff() ? r : 0.f);
+}
+
+// Offset of glu column n's hi value in a glu row of the pair layout (its lo value is 64 further).
+__device__ __forceinline__ int glu_pair_col(int n) { return 128 * (n >> 6) + (n & 63); }
 
 __device__ __forceinline__ u32x4 ld_global_16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -157,7 +178,8 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
 #pragma unroll
             for (int i = 0; i < kV3APer; ++i) dma16(a_src[i] + kt * kBK, sa + i * (kV3Waves * 1024));
 #pragma unroll
-            for (int i = 0; i < kV3BPer; ++i) dma16(b_src[i] + kt * kBK, sa + kV3ABytes + i * (kV3Waves * 1024));
+            for (int i = 0; i < kV3BPer; ++i)
+                dma16(b_src[i] + (kt >> prm.b_kshift) * kBK, sa + kV3ABytes + i * (kV3Waves * 1024));
         };
 
         f32x16 acc[2][2];
@@ -216,7 +238,7 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
         // ---- epilogue through LDS. Accumulator element r of a 32x32 block sits at
         // row 8*(r/4) + 4*(lane/32) + (r%4), column lane & 31.
         if constexpr (MODE == kModeGateUp) {
-            uint16_t* stg = reinterpret_cast<uint16_t*>(smem);  // [128][kV3GStride] bf16 glu tile
+            uint16_t* stg = reinterpret_cast<uint16_t*>(smem);  // [2][128][kV3GStride]: the hi tile, the lo tile
             const int c = wn * 32 + (lane & 31);                 // glu column within the tile
             float bg = 0.f, bu = 0.f;
             if constexpr (HAS_BIAS) {
@@ -229,17 +251,22 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    stg[row * kV3GStride + c] = f32_to_bf16_bits(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu));
+                    uint16_t hi, lo;
+                    split_bf16(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu), hi, lo);
+                    stg[row * kV3GStride + c] = hi;
+                    stg[(kV3BM + row) * kV3GStride + c] = lo;
                 }
             __syncthreads();
             uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            constexpr int kChunks = kV3BN / 2 / 8;  // 16-byte chunks per glu row (16)
-            for (int i = tid; i < kV3BM * kChunks; i += kV3Threads) {
-                const int row = i / kChunks, ch = i - row * kChunks;
+            constexpr int kChunks = kV3BN / 2 / 8;  // 16-byte chunks per glu row and half (16)
+            for (int i = tid; i < kV3BM * 2 * kChunks; i += kV3Threads) {
+                const int row = i / (2 * kChunks), rem = i - row * (2 * kChunks);
+                const int half = rem / kChunks, ch = rem - half * kChunks;  // half 0: hi, 1: lo
                 const int n = n0 + ch * 8;
                 if (row < rows && n < prm.N)
-                    *reinterpret_cast<u32x4*>(glu + (long long)(row_begin + row) * prm.F + n) =
-                        *reinterpret_cast<const u32x4*>(stg + row * kV3GStride + ch * 8);
+                    *reinterpret_cast<u32x4*>(glu + (long long)(row_begin + row) * 2 * prm.F + glu_pair_col(n) +
+                                              64 * half) =
+                        *reinterpret_cast<const u32x4*>(stg + (half * kV3BM + row) * kV3GStride + ch * 8);
             }
         } else {
             float* stg = reinterpret_cast<float*>(smem);  // [128][kV3YStride] fp32 tile
@@ -351,12 +378,13 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams pr
         auto load_regs = [&](int kt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) ra[i] = ld_global_16(a_src[i] + kt * kBK);
+            const int kb = kt >> prm.b_kshift;  // B's k-chunk
             if constexpr (!kBNcontig) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + kt * kBK);
+                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + kb * kBK);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + (long long)kt * kBK * prm.ldb);
+                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + (long long)kb * kBK * prm.ldb);
             }
         };
         auto store_lds = [&](int buf) {
@@ -439,8 +467,11 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams pr
                     for (int r = 0; r < 16; ++r) {
                         const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                         if (row < rows) {
-                            const float v = swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu);
-                            glu[(long long)(row_begin + row) * prm.F + n] = f32_to_bf16_bits(v);
+                            uint16_t hi, lo;
+                            split_bf16(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu), hi, lo);
+                            uint16_t* g = glu + (long long)(row_begin + row) * 2 * prm.F + glu_pair_col(n);
+                            g[0] = hi;
+                            g[64] = lo;
                         }
                     }
             }
@@ -606,6 +637,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g1.n_tiles = concat ? ceil_div(F, kV3BN / 2) : ceil_div(F, kBN / 2);
     g1.expert_stride = 2LL * F * H;
     g1.ldb = concat ? H : 2 * F;
+    g1.b_kshift = 0;
     st = launch_gateup(g1, layout, act, b1 != nullptr, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(2);
@@ -614,7 +646,8 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g2.B = static_cast<const uint16_t*>(w2);
     g2.bias = b2;
     g2.out = Y;
-    g2.Kdim = F;
+    g2.Kdim = 2 * F;  // the glu pair: 2F bf16 values per row
+    g2.b_kshift = 1;
     g2.N = H;
     g2.n_tiles = concat ? ceil_div(H, kV3BN) : ceil_div(H, kBN);
     g2.expert_stride = (long long)H * F;

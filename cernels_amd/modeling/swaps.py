@@ -8,11 +8,13 @@ model in place and ``"stock"`` restores the class forward. Variants per model ar
 ``SWAPS`` in sweep order, stock first. Only the MoE-experts part of the reference's swaps is
 here; its SAM rel-pos and vision-tower variants are other kernels.
 
-Decode dispatch: a call uses the decode GEMV whenever the GEMV takes it (at most
-``DECODE_MAX_TOKENS`` tokens and ``DECODE_MAX_PAIRS`` routed (token, slot) pairs, the limits of
-``cernels_moe_experts_decode``), else the prefill GEMM. The reference switches at 4 tokens
-(swaps.py:13). The gfx950 GEMV streams every distinct selected expert once, so up to its limits it
-is the faster entry: measured through the ops with the weights rotated over three copies, 66 against
+Decode dispatch: with the decode entry enabled (variant ``custom``), a call uses the decode GEMV
+whenever the GEMV takes it (at most ``DECODE_MAX_TOKENS`` tokens and ``DECODE_MAX_PAIRS`` routed
+(token, slot) pairs, the limits of ``cernels_moe_experts_decode``), else the prefill GEMM. Without it
+(``custom_prefill``) the reference's switch stays: calls of at most ``REFERENCE_DECODE_TOKENS`` tokens
+run the module's own forward and every longer call the prefill op (src/modeling/swaps.py:13,20-27), so a
+custom_prefill measurement means what the reference's does. The gfx950 GEMV streams every distinct
+selected expert once, so up to its limits it is the faster entry: measured through the ops with the weights rotated over three copies, 66 against
 98 us at 16 tokens and 95 against 109 us at 32 on the deepseek-v2-lite expert shapes (k=6), 135
 against 166 us and 183 against 212 us on the 30B-A3B shapes (k=8).
 """
@@ -24,6 +26,7 @@ from importlib import import_module
 
 DECODE_MAX_TOKENS = 64   # cernels_moe_decode_max_tokens()
 DECODE_MAX_PAIRS = 256   # cernels_moe_decode_max_pairs()
+REFERENCE_DECODE_TOKENS = 4  # the reference's decode switch (src/modeling/swaps.py:13)
 
 
 def use_decode(tokens: int, top_k: int) -> bool:
@@ -66,7 +69,11 @@ def _dispatching_forward(module, prefill_op, decode_op):
     stock = type(module).forward
 
     def forward(hidden, top_k_index, top_k_weights):
-        op = decode_op if use_decode(hidden.size(0), top_k_index.size(-1)) else prefill_op
+        tokens = hidden.size(0)
+        if decode_op is not None:
+            op = decode_op if use_decode(tokens, top_k_index.size(-1)) else prefill_op
+        else:
+            op = None if tokens <= REFERENCE_DECODE_TOKENS else prefill_op
         if op is None:
             return stock(module, hidden, top_k_index, top_k_weights)
         return op(hidden, top_k_index, top_k_weights, module)

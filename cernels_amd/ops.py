@@ -319,37 +319,52 @@ def route(indices: torch.Tensor, num_experts: int, tile_m: int = 128):
 
 # ---- the reference's per-model torch ops (same schemas) ---------------------------------------
 #
-# Prefill runs on packed weights: the first call with a given weight tensor packs it (one launch per
-# projection) and keeps the packed copy for as long as that tensor lives, keyed on its storage
-# pointer and in-place version counter (a write through ``.data`` does not advance the counter: call
-# ``forget_packed(gate_up_proj)`` after one). Decode reads the weights as stored.
+# Prefill runs on packed weights: the first call with a given set of weight tensors packs them (one
+# launch per projection) and keeps the packed copy for as long as gate_up_proj lives. The copy is used
+# again only for the very same tensor objects (held as weak references and compared by identity) at
+# the same storage pointer, in-place version counter and shape; a write through ``.data`` does not
+# advance the counter: call ``forget_packed(gate_up_proj)`` after one. Memory: the packed copy holds
+# as many bytes as the expert weights themselves (plus a table of one byte per 32 down columns), so
+# while it is kept the experts occupy about twice their own size in HBM. Decode reads the weights as
+# stored.
 
 import weakref
 
-# id(gate_up_proj) -> (weakref to it, key, PackedExperts); an entry goes when its tensor is freed.
-# (Tensors compare elementwise, so a WeakKeyDictionary cannot key on them; identity is what is meant.)
+# id(gate_up_proj) -> (weak references to the keyed tensors, key, PackedExperts); an entry goes when
+# gate_up_proj is freed. (Tensors compare elementwise, so a WeakKeyDictionary cannot key on them;
+# identity is what is meant.)
 _PACKED: dict = {}
 
 
+def _weak(t):
+    return None if t is None else weakref.ref(t)
+
+
+def _same_objects(refs, tensors) -> bool:
+    return all((r is None and t is None) or (r is not None and t is not None and r() is t)
+               for r, t in zip(refs, tensors))
+
+
 def _packed_for(gate_up_proj, down_proj, layout, act, gate_up_bias=None, down_bias=None) -> PackedExperts:
-    key = tuple(None if t is None else (t.data_ptr(), t._version, tuple(t.shape))
-                for t in (gate_up_proj, down_proj, gate_up_bias, down_bias)) + (layout, act)
+    tensors = (gate_up_proj, down_proj, gate_up_bias, down_bias)
+    key = tuple(None if t is None else (t.data_ptr(), t._version, tuple(t.shape)) for t in tensors) + (layout, act)
     hit = _PACKED.get(id(gate_up_proj))
-    if hit is not None and hit[0]() is gate_up_proj and hit[1] == key:
+    if hit is not None and _same_objects(hit[0], tensors) and hit[1] == key:
         return hit[2]
     with torch.no_grad():
         pk = pack_experts(gate_up_proj, down_proj, layout=layout, act=act, gate_up_bias=gate_up_bias,
                           down_bias=down_bias)
     tid = id(gate_up_proj)
-    ref = weakref.ref(gate_up_proj, lambda _r, tid=tid: _PACKED.pop(tid, None))
-    _PACKED[tid] = (ref, key, pk)
+    refs = (weakref.ref(gate_up_proj, lambda _r, tid=tid: _PACKED.pop(tid, None)),) + tuple(
+        _weak(t) for t in tensors[1:])
+    _PACKED[tid] = (refs, key, pk)
     return pk
 
 
 def packed_copy(gate_up_proj) -> PackedExperts | None:
     """The packed copy kept for ``gate_up_proj``, if any."""
     hit = _PACKED.get(id(gate_up_proj))
-    return hit[2] if hit is not None and hit[0]() is gate_up_proj else None
+    return hit[2] if hit is not None and hit[0][0]() is gate_up_proj else None
 
 
 def forget_packed(gate_up_proj) -> None:

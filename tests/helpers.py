@@ -95,3 +95,49 @@ def assert_within_tolerance(out, ref64, what="", strict=False):
 def assert_reference_verify(out, eager, what=""):
     ok = torch.allclose(out.float().cpu(), eager.float().cpu(), atol=2e-2, rtol=2e-2)
     assert ok, f"{what}: fails the reference's allclose(atol=rtol=2e-2) against op_eager"
+
+
+# ---- whole-output strict bar at full BASELINE / reference sizes ----------------------------------------
+
+_FULL_CASES: dict = {}
+
+
+def full_case(name, device):
+    """(case on the CPU, its device tensors, the exact fp64 output on the device) of a BASELINE or reference
+    workload, built once per process. The exact value is the float64 restatement (the oracle, a checker
+    only) computed on the GPU in float64."""
+    hit = _FULL_CASES.get(name)
+    if hit is not None:
+        return hit
+    from cernels_amd.configs.registry import BASELINE_SHAPES, REFERENCE_SHAPES
+    from cernels_amd.configs.synth import make_inputs, make_weights
+
+    s = BASELINE_SHAPES.get(name) or REFERENCE_SHAPES[name]
+    print(f"[full case {name}] generating", flush=True)
+    inp, wts = make_inputs(s), make_weights(s)
+    c = dict(x=inp.x, idx=inp.top_k_index, w=inp.top_k_weights, W1=wts.gate_up_proj, W2=wts.down_proj,
+             b1=wts.gate_up_proj_bias, b2=wts.down_proj_bias, layout=s.layout, act=s.act)
+    d = to_device(c, device)
+    print(f"[full case {name}] fp64 oracle on the GPU", flush=True)
+    mv = lambda t: None if t is None else t.to(device)  # noqa: E731
+    ref = O.experts_fp64(mv(c["x"]), mv(c["idx"]), mv(c["w"]), mv(c["W1"]), mv(c["W2"]), mv(c["b1"]), mv(c["b2"]),
+                         layout=s.layout, act=s.act)
+    _FULL_CASES.clear()  # one workload resident at a time
+    _FULL_CASES[name] = (c, d, ref)
+    return c, d, ref
+
+
+def assert_strict_full(out, ref, what=""):
+    """The north-star bar on a whole output, with no allowance: max|out - exact| <= 2e-2 * RMS(exact), or the
+    correctly rounded answer bf16(exact)'s own max error where that is larger (no bf16 output can do better;
+    it happens on the reference's deepseek routing, whose weights are not renormalised). Returns
+    (error, floor, bar), each relative to RMS(exact)."""
+    out = out.to(ref.device).double()
+    rms = float(ref.pow(2).mean().sqrt())
+    err = float((out - ref).abs().max()) / rms
+    floor = float((ref.to(torch.bfloat16).double() - ref).abs().max()) / rms
+    bar = max(TOL_RMS, floor)
+    print(f"[strict {what}] max|err|/RMS = {err:.6f} (correctly rounded bf16: {floor:.6f}; bar {bar:.6f})",
+          flush=True)
+    assert err <= bar, f"{what}: max|err| = {err:.6f} RMS > {bar:.6f} RMS (bf16(exact) reads {floor:.6f})"
+    return err, floor, bar

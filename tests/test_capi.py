@@ -35,7 +35,7 @@ def test_workspace_sizes(L):
     a = L.cernels_moe_experts_workspace_bytes(2048, 1280, 896, 64, 6)
     b = L.cernels_moe_experts_workspace_bytes(4096, 1280, 896, 64, 6)
     P = 2048 * 6
-    assert a >= P * 896 * 2 + P * 1280 * 4  # glu bf16 + weighted down rows fp32
+    assert a >= P * 896 * 4 + P * 1280 * 4  # glu as bf16 pairs + weighted down rows fp32
     assert b > a
     assert L.cernels_moe_experts_workspace_bytes(-1, 1280, 896, 64, 6) == 0
     assert L.cernels_moe_experts_decode_workspace_bytes(1, 2048, 768, 128, 8) >= 8 * 768 * 2  # glu bf16
@@ -91,3 +91,19 @@ def test_per_model_entries_check_arguments(L):
     for name in ("cernels_cohere2_moe_experts_decode", "cernels_deepseek_ocr2_moe_experts_decode"):
         assert getattr(L, name)(p, p, p, p, p, 4, 128, 64, 8, 2, p, p, ws, None) == 4
     assert L.cernels_gpt_oss_moe_experts(p, p, p, p, p, p, p, 4, 128, 64, 8, 2, p, p, ws, None) == 4
+
+
+def test_noalloc_decode_refuses_what_the_decode_entry_refuses(L):
+    """The allocation-free entry runs the decode entry's checks, in its order, before its scratch-size
+    check: every refused call returns the decode entry's status, whatever F is."""
+    p = _fake()
+    cases = [dict(T=1, F=128, K=257), dict(T=1, F=4096, K=257), dict(T=65, F=4096, K=1), dict(T=4, F=4104, K=2),
+             dict(T=4, F=64, K=2, layout=1), dict(T=-1, F=64, K=2), dict(T=4, F=64, K=2, act=9)]
+    for c in cases:
+        args = (p, p, None, p, None, p, p, c["T"], 256, c["F"], 8, c["K"], c.get("layout", 0), c.get("act", 0), p)
+        want = L.cernels_moe_experts_decode(*args, p, ctypes.c_size_t(1 << 40), None)
+        assert want != 0, c
+        assert L.cernels_moe_experts_decode_noalloc(*args, None) == want, c
+    mis = (_fake(0x10002), p, None, p, None, p, p, 1, 256, 128, 8, 2, 0, 0, p)
+    assert L.cernels_moe_experts_decode_noalloc(*mis, None) == 3  # misaligned x, as the decode entry says
+    assert L.cernels_moe_experts_decode_noalloc(p, p, None, p, None, p, p, 0, 256, 128, 8, 2, 0, 0, p, None) == 0

@@ -48,8 +48,10 @@ def test_install_dispatch_and_restore():
     assert _calls(m, 64, K=4) == ["d", "d"]
     assert _calls(m, 65, K=1) == ["p", "p"]
     assert seen[0][2] is m.layers[0]["experts"] and seen[1][2] is m.layers[1]["experts"]
-    swaps.install(m, "Cohere2MoeExperts", prefill, None)  # prefill only: decode-sized calls stay stock
+    swaps.install(m, "Cohere2MoeExperts", prefill, None)  # prefill only: the reference's 4-token switch
     assert _calls(m, 1) == [("stock", 1)] * 2
+    assert _calls(m, 4) == [("stock", 4)] * 2
+    assert _calls(m, 5) == ["p", "p"]  # above 4 tokens, even where the decode GEMV would take the call
     assert _calls(m, 100) == ["p", "p"]
     swaps.install(m, "Cohere2MoeExperts", None, None)  # restore
     assert "forward" not in vars(m.layers[0]["experts"])
