@@ -30,10 +30,13 @@
 // as fp16 too (MFMA operands share one type), each 32-column fragment scaled by a power of two so its
 // largest |w| sits in [2^14, 2^15): the conversion from bf16 is exact there, and the epilogue
 // multiplies the fragment's columns back by that power of two. A glu segment (a row's 16 or 32
-// columns of one GEMM1 wave) whose largest |glu| reaches 2^15 is stored scaled by 2^-s (s >= 1, so it
-// cannot overflow fp16) and its row is marked; a small kernel between the two GEMMs then brings every
-// marked row to one scale and records it, which GEMM2 folds into the row's routing weight. Without
-// such rows (the normal case) that kernel reads one flag and exits.
+// columns of one GEMM1 wave) whose largest |glu| m reaches 2^15 is stored scaled by 2^-s (s >= 1, so it
+// cannot overflow fp16), and so is a segment with 0 < m < 2^-8 (s <= -23: scaled up, so its values do
+// not fall into fp16's subnormals, whose fixed 2^-24 spacing would leave small rows with a large
+// relative error); both put m * 2^-s in [2^14, 2^15) and mark the row. An all-zero segment records
+// kGluAnyScale (it is exact at every scale). A small kernel between the two GEMMs then brings every
+// marked row to its segments' largest s and records it per pair; the combine multiplies that pair's
+// row by 2^s. Without marked rows (the normal case) that kernel reads one flag and exits.
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -50,6 +53,10 @@ constexpr int kPkABytes = kPkBM * kBK * 2;  // 32 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
 constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
 constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
+// glu segments: scaled up below this largest |glu| (2^-8), down at or above 2^15; an all-zero segment
+// records kGluAnyScale in gexp
+constexpr float kGluSmall = 0.00390625f;
+constexpr int kGluAnyScale = -128;
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -216,6 +223,7 @@ struct PkParams {
     int fw;                        // fragments per item (<= kPkWaves); waves past fw idle
     int* counters;                 // [8] per-XCD work counters, zeroed by the route kernel
     int8_t* gexp;                  // GEMM1: [F/16, p_cap] exponent of each 16-column glu row segment
+                                   // (kGluAnyScale: all zero)
     int8_t* rsig;                  // [P] per glu row: 0, or (GEMM1) 1 = has a scaled segment, then its scale
     int32_t* sync;                 // [2]: [1] = "some glu segment is scaled"; zeroed by the route kernel
     int p_cap;                     // row stride of gexp (T*K)
@@ -570,11 +578,17 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         if (active) {
             const int c4 = 4 * (lane >> 5);
             // glu stores: fp16 segments (16 columns per lane pair for gate_up, 32 for the non-gated
-            // projection), each with its power of two s in gexp: 0, unless some |glu| of the segment is
-            // 2^15 or more (or not finite); then the segment is stored again, scaled by 2^-s.
+            // projection), each with its power of two s in gexp: 0, unless the segment's largest |glu| m
+            // is 2^15 or more (or not finite) or below 2^-8 (and not 0); then the segment is stored
+            // again, scaled by 2^-s. m = 0 records kGluAnyScale. fmaxf passes over nan values.
             uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            auto glu_scale = [](float m) {  // s >= 1 with m * 2^-s < 2^15 (m >= 2^15, or inf: s = 1)
-                return max(1, __builtin_amdgcn_frexp_expf(m) - 15);
+            auto needs_scale = [](float m) { return !(m < 32768.f) || (m < kGluSmall && m > 0.f); };
+            // s with m * 2^-s in [2^14, 2^15): s >= 1 for m >= 2^15 (inf or nan: s = 1), s <= -23 for
+            // 0 < m < 2^-8 (clamped at -126, so 2^s stays a normal fp32 and s an int8 other than
+            // kGluAnyScale)
+            auto glu_scale = [](float m) {
+                const int s = __builtin_amdgcn_frexp_expf(m) - 15;
+                return m < 32768.f ? max(-126, s) : max(1, s);
             };
             auto mark_scaled = [&](long long r) {
                 if (lane < 32) prm.rsig[r] = 1;
@@ -606,25 +620,24 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     if (row < rows) {  // lanes l and l ^ 32 hold the same row
                         const long long r = row_begin + row;
                         uint16_t* g = glu + r * prm.F + 16 * fc + c4;
-                        bool big = false;
+                        // the segment's largest |glu|; a nan is passed over (it reaches the output as a nan
+                        // at any scale), an inf is not (scaled down, it keeps finite values finite)
+                        float m = 0.f;
 #pragma unroll
                         for (int i = 0; i < 2; ++i) {
                             float v[4];
                             glu4(mb, i, v);
-                            big |= !(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) < 32768.f);
+#pragma unroll
+                            for (int jj = 0; jj < 4; ++jj) m = fmaxf(m, fabsf(v[jj]));
                             *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
                         }
-                        if (lane < 32) prm.gexp[(long long)fc * prm.p_cap + r] = 0;
-                        if (__shfl_xor((int)big, 32, kWave) | (int)big) {  // rare: store the segment scaled
+                        m = fmaxf(m, __shfl_xor(m, 32, kWave));  // the same on both lanes of the row
+                        if (lane < 32) prm.gexp[(long long)fc * prm.p_cap + r] = (int8_t)(m == 0.f ? kGluAnyScale : 0);
+                        if (needs_scale(m)) {  // rare: store the segment scaled
                             float v[2][4];
-                            float m = 0.f;
 #pragma unroll
-                            for (int i = 0; i < 2; ++i) {
-                                glu4(mb, i, v[i]);
-#pragma unroll
-                                for (int jj = 0; jj < 4; ++jj) m = fmaxf(m, fabsf(v[i][jj]));
-                            }
-                            const int sg = glu_scale(fmaxf(m, __shfl_xor(m, 32, kWave)));
+                            for (int i = 0; i < 2; ++i) glu4(mb, i, v[i]);
+                            const int sg = glu_scale(m);
 #pragma unroll
                             for (int i = 0; i < 2; ++i)
                                 *reinterpret_cast<u32x2*>(g + 8 * i) =
@@ -645,24 +658,27 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     if (row < rows) {  // lanes l and l ^ 32 hold the same row
                         const long long r = row_begin + row;
                         uint16_t* g = glu + r * prm.F + 32 * fc + c4;
-                        bool big = false;
+                        // the segment's largest |glu|; a nan is passed over (it reaches the output as a nan
+                        // at any scale), an inf is not (scaled down, it keeps finite values finite)
+                        float m = 0.f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             float v[4];
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj) v[jj] = act_plain<ACT>(acc[mb][4 * i + jj]);
-                            big |= !(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))) < 32768.f);
+                            for (int jj = 0; jj < 4; ++jj) {
+                                v[jj] = act_plain<ACT>(acc[mb][4 * i + jj]);
+                                m = fmaxf(m, fabsf(v[jj]));
+                            }
                             *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
                         }
+                        m = fmaxf(m, __shfl_xor(m, 32, kWave));  // the same on both lanes of the row
                         if (lane < 32) {
-                            prm.gexp[(long long)(2 * fc) * prm.p_cap + r] = 0;
-                            prm.gexp[(long long)(2 * fc + 1) * prm.p_cap + r] = 0;
+                            const int8_t s0 = (int8_t)(m == 0.f ? kGluAnyScale : 0);
+                            prm.gexp[(long long)(2 * fc) * prm.p_cap + r] = s0;
+                            prm.gexp[(long long)(2 * fc + 1) * prm.p_cap + r] = s0;
                         }
-                        if (__shfl_xor((int)big, 32, kWave) | (int)big) {  // rare: store the segment scaled
-                            float m = 0.f;
-#pragma unroll
-                            for (int q = 0; q < 16; ++q) m = fmaxf(m, fabsf(act_plain<ACT>(acc[mb][q])));
-                            const int sg = glu_scale(fmaxf(m, __shfl_xor(m, 32, kWave)));
+                        if (needs_scale(m)) {  // rare: store the segment scaled
+                            const int sg = glu_scale(m);
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
                                 float v[4];
@@ -812,10 +828,11 @@ __global__ __launch_bounds__(1024) void moe_combine_h_kernel(const unsigned char
 }
 
 // Between the GEMMs: glu rows with a segment stored scaled (rsig[r] != 0, marked by GEMM1) are brought
-// to the row's largest segment scale s_r (the other segments rescaled by 2^-(s_r - s_u), fp16 round
-// to nearest); rsig[r] = s_r (GEMM2 scales a bias by 2^-s_r for that row) and psig[pair] = s_r for
-// every valid pair (the combine multiplies the pair's Y row by 2^s_r). Exits at once unless GEMM1
-// marked some row (sync[1]).
+// to the largest scale s_r of the row's segments (all-zero segments, kGluAnyScale, take any scale and
+// are left alone; the others are rescaled by 2^-(s_r - s_u), fp16 round to nearest), and psig[pair] =
+// s_r for every valid pair (the combine multiplies the pair's Y row by 2^s_r; the down bias is added
+// there unscaled). rsig[r] is only the mark; it is set to s_r for inspection and read by no kernel.
+// Exits at once unless GEMM1 marked some row (sync[1]).
 __global__ __launch_bounds__(256) void moe_glu_fixup_kernel(uint16_t* __restrict__ glu, const int8_t* __restrict__ gexp,
                                                             int8_t* __restrict__ rsig, int8_t* __restrict__ psig,
                                                             const int32_t* __restrict__ sorted_pairs,
@@ -828,11 +845,12 @@ __global__ __launch_bounds__(256) void moe_glu_fixup_kernel(uint16_t* __restrict
             psig[sorted_pairs[r]] = 0;
             continue;
         }
-        int smax = 0;
+        int smax = kGluAnyScale;  // a marked row has a scaled segment, so smax ends above kGluAnyScale
         for (int u = 0; u < U16; ++u) smax = max(smax, (int)gexp[(long long)u * p_cap + r]);
         for (int u = 0; u < U16; ++u) {
-            const int d = smax - gexp[(long long)u * p_cap + r];
-            if (d == 0) continue;
+            const int su = gexp[(long long)u * p_cap + r];
+            const int d = smax - su;
+            if (d == 0 || su == kGluAnyScale) continue;
             uint16_t* g = glu + (long long)r * F + 16 * u;
             for (int j = 0; j < 16; ++j) {
                 const float v = (float)__builtin_bit_cast(_Float16, g[j]);

@@ -16,7 +16,8 @@ import pytest
 import torch
 
 from conftest import GOLDEN_NAMES, load_golden
-from helpers import assert_reference_verify, assert_within_tolerance, oracle_eager, oracle_fp64, rand_case, run_gpu, to_device
+from helpers import (assert_reference_verify, assert_strict_full, assert_within_tolerance, full_case, oracle_eager,
+                     oracle_fp64, rand_case, run_gpu, to_device)
 
 pytestmark = pytest.mark.gpu
 
@@ -217,32 +218,9 @@ def test_packed_full_output_strict(device, name):
     exact value being the float64 restatement of the op on the same bf16 inputs (computed on the GPU in
     float64 by the oracle; checker only). The correctly rounded answer bf16(exact) is measured beside it,
     as the floor any bf16 output has."""
-    from cernels_amd.configs.registry import BASELINE_SHAPES, REFERENCE_SHAPES
-    from cernels_amd.configs.synth import make_inputs, make_weights
-    from oracle import eager as O
-
-    s = BASELINE_SHAPES.get(name) or REFERENCE_SHAPES[name]
-    print(f"[strict full {name}] generating", flush=True)
-    inp, wts = make_inputs(s), make_weights(s)
-    c = dict(x=inp.x, idx=inp.top_k_index, w=inp.top_k_weights, W1=wts.gate_up_proj, W2=wts.down_proj,
-             b1=wts.gate_up_proj_bias, b2=wts.down_proj_bias, layout=s.layout, act=s.act)
-    d = to_device(c, device)
-    out = _run_packed(c, device, d).double()
-    print(f"[strict full {name}] fp64 oracle on the GPU", flush=True)
-    mv = lambda t: None if t is None else t.to(device)  # noqa: E731
-    ref = O.experts_fp64(mv(c["x"]), mv(c["idx"]), mv(c["w"]), mv(c["W1"]), mv(c["W2"]), mv(c["b1"]), mv(c["b2"]),
-                         layout=s.layout, act=s.act)
-    rms = float(ref.pow(2).mean().sqrt())
-    err = float((out - ref).abs().max()) / rms
-    print(f"[strict full {name}] max|exact|/RMS = {float(ref.abs().max()) / rms:.1f}", flush=True)
-    floor = float((ref.to(torch.bfloat16).double() - ref).abs().max()) / rms
-    # The bar is 2e-2*RMS, or the correctly rounded answer's own max error where that is larger (no bf16
-    # output can do better; it happens on the reference's deepseek routing, whose weights are not
-    # renormalised).
-    bar = max(2e-2, floor)
-    print(f"[strict full {name}] max|err|/RMS = {err:.6f} (correctly rounded bf16: {floor:.6f}; bar {bar:.6f})",
-          flush=True)
-    assert err <= bar, f"{name}: max|err| = {err:.6f} RMS > {bar:.6f} RMS (bf16(exact) reads {floor:.6f})"
+    c, d, ref = full_case(name, device)
+    out = _run_packed(c, device, d)
+    assert_strict_full(out, ref, f"packed {name}")
 
 
 def _scaled_rows_case(seed, T, H, Fi, E, K, big_rows, gain, bias=False):
@@ -272,6 +250,50 @@ def test_glu_beyond_fp16_range_is_rescaled(device, gain, bias):
     assert_within_tolerance(out[small], ref[small], f"other rows gain {gain}")
 
 
+@pytest.mark.parametrize("gain", [1e-3, 1e-4])
+def test_small_glu_is_rescaled(device, gain):
+    """glu is stored in fp16, whose subnormals (below 2^-14) have a fixed 2^-24 spacing: a row of tiny glu
+    values would lose most of its precision. Segments whose largest |glu| is below 2^-8 are stored scaled
+    up, and the row is brought to one scale as above. Rows of x multiplied by `gain` (glu ~ gain^2:
+    3e-7 and 3e-9 here) must each meet the bar on their own scale; so must the rows left alone."""
+    T, H, Fi, E, K = 300, 256, 192, 8, 3
+    tiny = torch.arange(5, T, 23)
+    c = _scaled_rows_case(13, T, H, Fi, E, K, tiny, gain)
+    out = _run_packed(c, device).cpu()
+    ref = oracle_fp64(c)
+    rest = torch.ones(T, dtype=torch.bool)
+    rest[tiny] = False
+    assert float(ref[tiny].abs().max()) < 1e-4 * float(ref[rest].abs().max())
+    assert_within_tolerance(out[tiny], ref[tiny], f"tiny rows gain {gain}", strict=True)
+    assert_within_tolerance(out[rest], ref[rest], f"other rows gain {gain}")
+
+
+def test_small_zero_and_normal_segments_in_one_row(device):
+    """Rows whose glu segments differ in scale: for two experts the gate and up weights of intermediate
+    columns 0-15 are multiplied by 1e-4 (a tiny segment beside normal ones: the row keeps scale 0 and the
+    tiny segment is brought back to it) and those of columns 16-31 are zero (an all-zero segment, exact at
+    any scale); rows of x scaled by 1e-3 then have only tiny and zero segments and are scaled up as a
+    whole. Every row group meets the bar on its own scale."""
+    T, H, Fi, E, K = 256, 128, 128, 4, 2
+    c = rand_case(14, T, H, Fi, E, K, std=0.05)
+    W1 = c["W1"].float()
+    for e in (0, 2):
+        for half in (0, Fi):  # gate rows, then the matching up rows
+            W1[e, half:half + 16] *= 1e-4
+            W1[e, half + 16:half + 32] = 0.0
+    c["W1"] = W1.bfloat16()
+    tiny = torch.arange(0, T, 9)
+    x = c["x"].float()
+    x[tiny] *= 1e-3
+    c["x"] = x.bfloat16()
+    out = _run_packed(c, device).cpu()
+    ref = oracle_fp64(c)
+    rest = torch.ones(T, dtype=torch.bool)
+    rest[tiny] = False
+    assert_within_tolerance(out[tiny], ref[tiny], "tiny rows with zero segments", strict=True)
+    assert_within_tolerance(out[rest], ref[rest], "rows with a tiny and a zero segment")
+
+
 def test_glu_beyond_fp16_range_nongated(device):
     """The non-gated first projection (megablocks' w1) with ReLU and rows of x scaled up: its fp16 glu
     segments of 32 columns take the same rescaling path."""
@@ -296,3 +318,28 @@ def test_glu_beyond_fp16_range_nongated(device):
     assert torch.isfinite(out.float()).all()
     assert_within_tolerance(out[big], ref[big], "relu scaled rows")
     assert_within_tolerance(out[small], ref[small], "relu other rows")
+
+
+def test_small_glu_nongated(device):
+    """The non-gated projection (ReLU: many all-zero 32-column segments) with rows of x scaled by 1e-4: the
+    tiny rows are scaled up past their zero segments and meet the bar on their own scale."""
+    from cernels_amd import ops
+    from oracle import eager as O
+
+    g = torch.Generator().manual_seed(15)
+    T, H, F, E, K = 200, 128, 192, 4, 2
+    x = torch.randn(T, H, generator=g)
+    tiny = torch.arange(1, T, 13)
+    x[tiny] *= 1e-4
+    x = x.bfloat16()
+    w1 = (torch.randn(E, H, F, generator=g) * 0.05).bfloat16()
+    w2 = (torch.randn(E, F, H, generator=g) * 0.05).bfloat16()
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).int()
+    wt = torch.rand(T, K, generator=g)
+    d = [t.contiguous().to(device) for t in (x, w1, w2, idx, wt)]
+    out = ops.megablocks_moe(*d, K, 2).cpu()
+    ref = O.megablocks_fp64(x, idx, wt, w1, w2, 2)
+    rest = torch.ones(T, dtype=torch.bool)
+    rest[tiny] = False
+    assert_within_tolerance(out[tiny], ref[tiny], "relu tiny rows", strict=True)
+    assert_within_tolerance(out[rest], ref[rest], "relu other rows")
