@@ -338,7 +338,7 @@ int decode_checks(const void* x, const void* w1, const void* w2, const int32_t* 
     if (st != CERNELS_MOE_OK || T == 0) return st;
     if (layout != CERNELS_MOE_LAYOUT_CONCAT || !act_gated(act)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     if (T > cmoe::decode_max_tokens() || T * K > cmoe::decode_max_pairs()) return CERNELS_MOE_UNSUPPORTED_SHAPE;
-    if (H % 8 || F % 8 || !cmoe::decode_shape_supported(H, F)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
+    if (H % 8 || F % 8 || E > kMaxExperts || !cmoe::decode_shape_supported(H, F)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
     return CERNELS_MOE_OK;
 }
 }  // namespace

@@ -59,6 +59,22 @@ def test_decode_cases(device, case):
         assert_within_tolerance(pre, out.double(), f"{case} prefill vs decode")
 
 
+def test_decode_many_distinct_experts(device):
+    """64 tokens x 4 slots over 1024 experts: up to 256 distinct experts, each with one or two pairs, and a
+    pair order of up to 256 entries."""
+    c = rand_case(12, 64, 256, 128, 1024, 4)
+    out = run_gpu(c, device, decode=True).cpu()
+    assert_within_tolerance(out, oracle_fp64(c), "E=1024")
+
+
+def test_decode_one_expert_for_all(device):
+    """Every token routes its K slots to the same K experts (U = K, every expert has all T tokens)."""
+    c = rand_case(13, 40, 512, 256, 16, 4)
+    c["idx"][:] = torch.tensor([3, 7, 11, 15])
+    out = run_gpu(c, device, decode=True).cpu()
+    assert_within_tolerance(out, oracle_fp64(c), "same experts")
+
+
 def test_decode_all_invalid(device):
     c = rand_case(9, 3, 256, 128, 4, 2)
     c["idx"][:] = -1
