@@ -106,6 +106,7 @@ class Bench:
         return [1e3 * t for t in m.times], m.number_per_run
 
     def measure(self, e: Entrant) -> TimingResults:
+        print(f"  {e.label}: {self.warmup} untimed calls", file=sys.stderr)  # a compile happens in these
         self.prime(e)
         verdict = self.check(e)
         times, per_block = self.sample(e)

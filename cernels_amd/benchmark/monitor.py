@@ -9,14 +9,29 @@ import sys
 from dataclasses import dataclass
 
 
+class _Tee(io.TextIOBase):
+    """Writes to a buffer and passes every write on to the stream it wraps, as it happens."""
+
+    def __init__(self, stream):
+        self.buf, self.stream = io.StringIO(), stream
+
+    def write(self, text):
+        self.buf.write(text)
+        self.stream.write(text)
+        self.stream.flush()
+        return len(text)
+
+    def getvalue(self):
+        return self.buf.getvalue()
+
+
 @contextlib.contextmanager
 def capture():
-    """Collects everything written to stderr inside the block (for the saved log) and writes it back out
-    when the block ends."""
-    buf = io.StringIO()
-    with contextlib.redirect_stderr(buf):
-        yield buf
-    sys.stderr.write(buf.getvalue())
+    """Collects everything written to stderr inside the block (for the saved log) while still showing it as it is
+    written (a long compile inside the block then shows its progress lines at once)."""
+    tee = _Tee(sys.stderr)
+    with contextlib.redirect_stderr(tee):
+        yield tee
 
 
 @dataclass
