@@ -11,10 +11,9 @@
 // error (0.0207 / 0.0226 / 0.0262 against the 2e-2*RMS bar on the deepseek-v2-lite, 30B-A3B and
 // qwen3-next Zipf workloads, by a float64 simulation of that rounding alone; with the pair the error
 // is the output's own bf16 rounding, 0.0127 / 0.0189 / 0.0183). A glu row is 2F bf16 values: per
-// 64 columns, the 64 hi values then the 64 lo values. GEMM2 reduces over those 2F values: stage s
-// reads A columns [64s, 64s + 64) and the weights of k-chunk s / 2 (b_kshift = 1), so every weight
-// chunk meets its glu twice, once as hi and once as lo. This doubles GEMM2's MFMAs and its weight
-// reads from L2; the weights still come from HBM once per tile.
+// 64 columns, the 64 hi values then the 64 lo values. A GEMM2 stage holds both halves of one 64-wide
+// k-chunk of glu beside that chunk's weights, and every weight fragment read from LDS feeds two MFMAs
+// (hi, then lo): GEMM2's MFMAs double, its weight loads do not.
 //
 // Replaces the reference's per-expert host loop (src/kops/cohere2_moe_experts/csrc/
 // cohere2_moe_experts.cu:315-358: gather_kernel, cublasGemmEx x2, swiglu_kernel,
@@ -58,14 +57,13 @@ struct GemmParams {
     const int32_t* meta;           // [0] = tiles
     const float* route_w;          // [P] fp32 routing weight per pair (GEMM2)
     void* out;                     // GEMM1: glu pairs bf16 [P, 2F]; GEMM2: Y fp32 [P, H]
-    int Kdim;                      // A's row length and the stages' span: H (GEMM1) or 2F (GEMM2)
+    int Kdim;                      // A's row length: H (GEMM1) or 2F (GEMM2, the glu pairs)
     int N;                         // output columns: F (GEMM1) or H (GEMM2)
     int F;                         // expert intermediate size
     int topk;
     int n_tiles;                   // output column tiles
     long long expert_stride;       // elements of one expert's matrix in B
     int ldb;                       // row stride of B (elements)
-    int b_kshift;                  // B's k-chunk of stage s is s >> b_kshift (GEMM2 reads the glu pair: 1)
 };
 
 // glu value v as the bf16 pair (hi, lo): hi = bf16(v), lo = bf16(v - hi) (lo = 0 where v is not finite).
@@ -111,14 +109,16 @@ constexpr int kV3BM = 128;
 constexpr int kV3BN = 256;
 constexpr int kV3Threads = 512;
 constexpr int kV3Waves = kV3Threads / kWave;
-constexpr int kV3Stages = 3;
 constexpr int kV3ABytes = kV3BM * kBK * 2;         // 16 KB
 constexpr int kV3BBytes = kV3BN * kBK * 2;         // 32 KB
-constexpr int kV3StageBytes = kV3ABytes + kV3BBytes;
-constexpr int kV3Lds = kV3Stages * kV3StageBytes;  // 144 KB
-constexpr int kV3APer = kV3BM / 8 / kV3Waves;      // 1 KB copies per wave per stage: A 2, B 4
+constexpr int kV3APer = kV3BM / 8 / kV3Waves;      // 1 KB copies per wave per stage: A 2 (or 4: hi, lo), B 4
 constexpr int kV3BPer = kV3BN / 8 / kV3Waves;
-constexpr int kV3CopiesPerStage = kV3APer + kV3BPer;
+// GEMM1: three stages of A 16 KB + B 32 KB; GEMM2: two stages of A hi 16 KB + A lo 16 KB + B 32 KB
+template <int MODE> constexpr int v3_stages() { return MODE == kModeDown ? 2 : 3; }
+template <int MODE> constexpr int v3_a_tiles() { return MODE == kModeDown ? 2 : 1; }
+template <int MODE> constexpr int v3_stage_bytes() { return v3_a_tiles<MODE>() * kV3ABytes + kV3BBytes; }
+constexpr int kV3Lds = 3 * (kV3ABytes + kV3BBytes);  // 144 KB (GEMM2 uses 128)
+static_assert(2 * (2 * kV3ABytes + kV3BBytes) <= kV3Lds, "GEMM2 stages fit the allocation");
 constexpr int kV3YStride = kV3BN + 4;              // fp32 epilogue row stride (bank offset per row)
 constexpr int kV3GStride = kV3BN / 2 + 8;          // bf16 epilogue row stride
 
@@ -173,13 +173,17 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
             }
             b_src[i] = Be + (long long)wrow * prm.ldb + ((lane & 7) ^ swz(r)) * 8;
         }
+        constexpr int S = v3_stages<MODE>(), AT = v3_a_tiles<MODE>(), SB = v3_stage_bytes<MODE>();
+        constexpr int kCopies = AT * kV3APer + kV3BPer;  // copies per wave per stage
         auto issue = [&](int kt, int stage) {
-            const uint32_t sa = lds0 + stage * kV3StageBytes + wave * 1024;
+            const uint32_t sa = lds0 + stage * SB + wave * 1024;
 #pragma unroll
-            for (int i = 0; i < kV3APer; ++i) dma16(a_src[i] + kt * kBK, sa + i * (kV3Waves * 1024));
+            for (int h = 0; h < AT; ++h)  // GEMM2: A columns [128 kt, 128 kt + 64) hi, then the lo half
 #pragma unroll
-            for (int i = 0; i < kV3BPer; ++i)
-                dma16(b_src[i] + (kt >> prm.b_kshift) * kBK, sa + kV3ABytes + i * (kV3Waves * 1024));
+                for (int i = 0; i < kV3APer; ++i)
+                    dma16(a_src[i] + kt * AT * kBK + h * kBK, sa + h * kV3ABytes + i * (kV3Waves * 1024));
+#pragma unroll
+            for (int i = 0; i < kV3BPer; ++i) dma16(b_src[i] + kt * kBK, sa + AT * kV3ABytes + i * (kV3Waves * 1024));
         };
 
         f32x16 acc[2][2];
@@ -200,26 +204,33 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
         }
         const int arow0 = wm * 64 + (lane & 31);
         const int khalf = lane >> 5;
-        const int nk = Kd / kBK;
+        const int nk = Kd / (AT * kBK);  // GEMM2: Kd = 2F, one stage per 64-wide k-chunk of glu
 
         wait_vmcnt<0>();  // index loads above must not be counted against the copies below
 #pragma unroll
-        for (int s = 0; s < kV3Stages - 1; ++s)
+        for (int s = 0; s < S - 1; ++s)
             if (s < nk) issue(s, s);
         for (int kt = 0; kt < nk; ++kt) {
-            if (kt + 1 < nk) wait_vmcnt<kV3CopiesPerStage>();  // stage kt+1 may stay in flight
-            else wait_vmcnt<0>();
+            if constexpr (S == 3) {
+                if (kt + 1 < nk) wait_vmcnt<kCopies>();  // stage kt+1 may stay in flight
+                else wait_vmcnt<0>();
+            } else {
+                wait_vmcnt<0>();  // two stages: stage kt+1 is issued after the barrier below
+            }
             __syncthreads();
-            if (kt + kV3Stages - 1 < nk) issue(kt + kV3Stages - 1, (kt + kV3Stages - 1) % kV3Stages);
-            const unsigned char* sA = smem + (kt % kV3Stages) * kV3StageBytes;
-            const unsigned char* sB = sA + kV3ABytes;
-            bf16x8 af[kBK / 16][2], bfr[kBK / 16][2];
+            if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+            const unsigned char* sA = smem + (kt % S) * SB;
+            const unsigned char* sB = sA + AT * kV3ABytes;
+            bf16x8 af[kBK / 16][2][AT], bfr[kBK / 16][2];
 #pragma unroll
             for (int ks = 0; ks < kBK / 16; ++ks) {
                 const int chunk = ks * 2 + khalf;
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb)
-                    af[ks][mb] = *reinterpret_cast<const bf16x8*>(sA + lds_off(arow0 + mb * 32, chunk));
+#pragma unroll
+                    for (int h = 0; h < AT; ++h)
+                        af[ks][mb][h] =
+                            *reinterpret_cast<const bf16x8*>(sA + h * kV3ABytes + lds_off(arow0 + mb * 32, chunk));
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
                     bfr[ks][nb] = *reinterpret_cast<const bf16x8*>(sB + lds_off(brow[nb] + (lane & 31), chunk));
@@ -230,8 +241,10 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
                 for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb)
-                        acc[mb][nb] =
-                            __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][mb], bfr[ks][nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+                        for (int h = 0; h < AT; ++h)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][mb][h], bfr[ks][nb],
+                                                                                  acc[mb][nb], 0, 0, 0);
         }
         __syncthreads();  // all waves are done reading the pipeline buffers; reuse them for the epilogue
 
@@ -304,9 +317,13 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
 template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
 __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams prm) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // LDS: A buffers 0,1 then B buffers 0,1, one 16 KB tile each
+    // LDS, 16 KB tiles: A buffers 0,1 then B buffers 0,1. GEMM2 (glu pairs): A (hi) buffers 0,1, one B
+    // buffer, A lo buffers 0,1: 80 KB, so two workgroups still fit a CU; the B buffer is rewritten only
+    // after a barrier that ends every wave's reads of it.
+    constexpr bool kPair = MODE == kModeDown;
     auto ldsA = [&](int buf) { return smem + buf * kTileBytes; };
-    auto ldsB = [&](int buf) { return smem + (2 + buf) * kTileBytes; };
+    auto ldsB = [&](int buf) { return smem + (2 + (kPair ? 0 : buf)) * kTileBytes; };
+    auto ldsL = [&](int buf) { return smem + (3 + buf) * kTileBytes; };
 
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int wm = wave & 1, wn = wave >> 1;
@@ -374,23 +391,29 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams pr
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-        u32x4 ra[4], rb[4];
+        constexpr int AT = kPair ? 2 : 1;  // A tiles per stage: glu hi and lo for GEMM2
+        u32x4 ra[AT][4], rb[4];
         auto load_regs = [&](int kt) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) ra[i] = ld_global_16(a_src[i] + kt * kBK);
-            const int kb = kt >> prm.b_kshift;  // B's k-chunk
+            for (int h = 0; h < AT; ++h)  // GEMM2: A columns [128 kt, 128 kt + 64) hi, then the lo half
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ra[h][i] = ld_global_16(a_src[i] + kt * AT * kBK + h * kBK);
             if constexpr (!kBNcontig) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + kb * kBK);
+                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + kt * kBK);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + (long long)kb * kBK * prm.ldb);
+                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + (long long)kt * kBK * prm.ldb);
             }
         };
-        auto store_lds = [&](int buf) {
+        auto store_a = [&](int buf) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u32x4*>(ldsA(buf) + lds_off((tid >> 3) + 32 * i, ac)) = ra[i];
+            for (int i = 0; i < 4; ++i) {
+                *reinterpret_cast<u32x4*>(ldsA(buf) + lds_off((tid >> 3) + 32 * i, ac)) = ra[0][i];
+                if constexpr (kPair) *reinterpret_cast<u32x4*>(ldsL(buf) + lds_off((tid >> 3) + 32 * i, ac)) = ra[AT - 1][i];
+            }
+        };
+        auto store_b = [&](int buf) {
             if constexpr (!kBNcontig) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
@@ -422,9 +445,10 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams pr
         const int arow0 = wm * 64 + (lane & 31);
         const int khalf = lane >> 5;
 
-        const int nk = Kd / kBK;
+        const int nk = Kd / (AT * kBK);  // GEMM2: Kd = 2F, one stage per 64-wide k-chunk of glu
         load_regs(0);
-        store_lds(0);
+        store_a(0);
+        store_b(0);
         __syncthreads();
         for (int kt = 0; kt < nk; ++kt) {
             const int buf = kt & 1;
@@ -432,10 +456,13 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams pr
 #pragma unroll
             for (int ks = 0; ks < kBK / 16; ++ks) {
                 const int chunk = ks * 2 + khalf;
-                bf16x8 af[2], bfr[2];
+                bf16x8 af[2][AT], bfr[2];
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-                    af[mb] = *reinterpret_cast<const bf16x8*>(ldsA(buf) + lds_off(arow0 + mb * 32, chunk));
+                for (int mb = 0; mb < 2; ++mb) {
+                    af[mb][0] = *reinterpret_cast<const bf16x8*>(ldsA(buf) + lds_off(arow0 + mb * 32, chunk));
+                    if constexpr (kPair)
+                        af[mb][AT - 1] = *reinterpret_cast<const bf16x8*>(ldsL(buf) + lds_off(arow0 + mb * 32, chunk));
+                }
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
                     bfr[nb] = *reinterpret_cast<const bf16x8*>(ldsB(buf) + lds_off(brow[nb] + (lane & 31), chunk));
@@ -443,9 +470,16 @@ __global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams pr
                 for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb], bfr[nb], acc[mb][nb], 0, 0, 0);
+#pragma unroll
+                        for (int h = 0; h < AT; ++h)
+                            acc[mb][nb] =
+                                __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb][h], bfr[nb], acc[mb][nb], 0, 0, 0);
             }
-            if (kt + 1 < nk) store_lds(buf ^ 1);
+            if (kt + 1 < nk) {
+                store_a(buf ^ 1);
+                if constexpr (kPair) __syncthreads();  // every wave is done with the one B buffer
+                store_b(buf ^ 1);
+            }
             __syncthreads();
         }
 
@@ -561,7 +595,14 @@ static hipError_t launch_gemm_t(const GemmParams& prm, int max_tiles, hipStream_
     } else {
         int grid = min(upper, cu_count() * 2);
         grid = ceil_div(max(grid, 1), 8) * 8;
-        const size_t lds = 4 * (size_t)kTileBytes;
+        const size_t lds = (MODE == kModeDown ? 5 : 4) * (size_t)kTileBytes;  // 80 KB (glu pairs) or 64 KB
+        static bool attr = false;
+        if (!attr) {  // above 64 KB of dynamic LDS the kernel has to allow it
+            hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>,
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (st != hipSuccess) return st;
+            attr = true;
+        }
         hipLaunchKernelGGL((moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>), dim3(grid), dim3(kGemmThreads), lds,
                            stream, prm);
     }
@@ -637,7 +678,6 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g1.n_tiles = concat ? ceil_div(F, kV3BN / 2) : ceil_div(F, kBN / 2);
     g1.expert_stride = 2LL * F * H;
     g1.ldb = concat ? H : 2 * F;
-    g1.b_kshift = 0;
     st = launch_gateup(g1, layout, act, b1 != nullptr, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(2);
@@ -647,7 +687,6 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g2.bias = b2;
     g2.out = Y;
     g2.Kdim = 2 * F;  // the glu pair: 2F bf16 values per row
-    g2.b_kshift = 1;
     g2.N = H;
     g2.n_tiles = concat ? ceil_div(H, kV3BN) : ceil_div(H, kBN);
     g2.expert_stride = (long long)H * F;
