@@ -53,6 +53,13 @@ constexpr int kPkABytes = kPkBM * kBK * 2;  // 32 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
 constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
 constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
+constexpr int kPkMaxTail = 16;              // most items split into halves at the end of an XCD's range
+// Items split at the end of each XCD's range: 12 for gate_up, none for down. Measured in one process against
+// no split (two alternations, µs per launch): gate_up 572.7/565.6 -> 559.4/557.3 on gpt-oss and 245.6/247.8 ->
+// 240.6/240.6 on the Zipf workload (16 and 24 items: within a few µs of 12); down 332.7/327.1 -> 339.3/339.9 on
+// gpt-oss, where a half item costs more of its full item's time (its activation tile and its weights are the
+// same) than the shorter tail gains.
+constexpr int kPkTailGateUp = 12;
 // glu segments: scaled up below this largest |glu| (2^-8), down at or above 2^15; an all-zero segment
 // records kGluAnyScale in gexp
 constexpr float kGluSmall = 0.00390625f;
@@ -228,6 +235,7 @@ struct PkParams {
     int32_t* sync;                 // [2]: [1] = "some glu segment is scaled"; zeroed by the route kernel
     int p_cap;                     // row stride of gexp (T*K)
     const int8_t* wexp;            // GEMM2: [E, NF] power of two of each packed fp16 weight fragment
+    int tail;                      // items at the end of an XCD's range handed out as two halves (<= kPkMaxTail)
 };
 
 
@@ -280,16 +288,37 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     // so the launch does not end on the slowest workgroup's fixed share. (Drawing from the other
     // XCDs' counters once the own one is exhausted was measured slower: the blocking draws and the
     // lost L2 sharing cost more than the balance gained.)
-    auto item_at = [&](int it, WorkItem& w) {  // it: global item index, or -1
-        if (it < 0) return false;
-        w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
+    //
+    // The tail: where an XCD's range holds at least three rounds of items, those of its last prm.tail items
+    // that have more than 3/4 kPkBM rows are handed out as two halves (rows [0, kPkBM/2) and the rest), so
+    // that the launch ends on shorter items. (Splitting items of fewer rows leaves a second half that costs
+    // nearly a whole item: 30B-A3B's gate_up, ~130-160 rows per expert, went from 181 to 200 µs.) Every row is
+    // still computed by one workgroup with the same k-loop, so the output is the same bit for bit. Work codes:
+    // 4 * item + h, h = 0 whole, 1 first half, 2 second half; offsets past the whole items index the tail
+    // table, built once per workgroup.
+    const int n_items = b_hi - b_lo;
+    const int n_tail = n_items >= 3 * slots ? min(min(prm.tail, kPkMaxTail), n_items) : 0;
+    const int n_whole = n_items - n_tail;  // >= 2 * slots, so the first two offsets never need the table
+    __shared__ int s_tail[2 * kPkMaxTail];
+    __shared__ int s_ntail;
+    auto item_at = [&](int code, WorkItem& w) {  // code: work code, or -1
+        if (code < 0) return false;
+        w = decode_item(code >> 2, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
+        if ((code & 3) == 1) {
+            w.rows = kPkBM / 2;
+        } else if ((code & 3) == 2) {
+            w.row_begin += kPkBM / 2;
+            w.rows -= kPkBM / 2;
+        }
         return true;
     };
-    auto item_of_off = [&](int off) {  // item at offset off of this XCD's range, or -1
-        const int it = b_lo + off;
-        return it < b_hi ? it : -1;
+    auto item_of_off = [&](int off) {  // work code at offset off of this XCD's work, or -1
+        if (off < n_whole) return 4 * (b_lo + off);
+        if (n_tail == 0) return -1;
+        const int t = off - n_whole;
+        return t < s_ntail ? s_tail[t] : -1;
     };
-    __shared__ int s_next;  // item after next (global index or -1), published once per item
+    __shared__ int s_next;  // work code of the item after next (or -1), published once per item
     // Operands are read with buffer loads: a 128-bit descriptor per operand and item (uniform,
     // SGPRs) plus a 32-bit per-lane offset, so the k-loop holds no 64-bit addresses.
     //   A: GEMM1 gathers token rows of x (descriptor over all of x); GEMM2 reads the item's own
@@ -404,6 +433,22 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         store_a(IC<kPkMB / 2>{}, IC<0>{});
     };
     start_item(cur, 0);
+    if (n_tail > 0 && wave == 0) {  // the tail table (read from the first item's end on; k-loop barriers order it)
+        const int it = b_lo + n_whole + lane;
+        bool split = false;
+        if (lane < n_tail) {
+            const WorkItem w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
+            split = w.rows > 3 * kPkBM / 4;
+        }
+        const uint64_t sb = __ballot(split);
+        const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+        const int pos = lane + __popcll(sb & lt);
+        if (lane < n_tail) {
+            s_tail[pos] = 4 * it + (split ? 1 : 0);
+            if (split) s_tail[pos + 1] = 4 * it + 2;
+        }
+        if (lane == 0) s_ntail = n_tail + __popcll(sb);
+    }
 
     int par = 0;  // LDS buffer / weight slot of the current item's stage 0
     for (int j = 0;; ++j) {
@@ -945,6 +990,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.rsig = rsig;
     g1.sync = meta + 24;
     g1.p_cap = T * K;
+    g1.tail = kPkTailGateUp;
     if (act == kActSilu)
         st = b1 ? launch_pk_t<kModePkGateUp, kActSilu, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActSilu, false>(g1, max_tiles, s);
@@ -976,6 +1022,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g2.n_tiles = nt2;
     g2.bounds = cost_split ? meta + 41 : nullptr;
     g2.bias = nullptr;  // the down bias is added by the combine
+    g2.tail = 0;
     st = launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(3);
