@@ -41,6 +41,7 @@
 #include <cmath>
 #include <type_traits>
 
+#include "moe_split.h"
 #include "moe_tile.h"
 
 namespace cmoe {
@@ -297,19 +298,14 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     // 4 * item + h, h = 0 whole, 1 first half, 2 second half; offsets past the whole items index the tail
     // table, built once per workgroup.
     const int n_items = b_hi - b_lo;
-    const int n_tail = n_items >= 3 * slots ? min(min(prm.tail, kPkMaxTail), n_items) : 0;
+    const int n_tail = tail_items(n_items, slots, prm.tail, kPkMaxTail);
     const int n_whole = n_items - n_tail;  // >= 2 * slots, so the first two offsets never need the table
     __shared__ int s_tail[2 * kPkMaxTail];
     __shared__ int s_ntail;
     auto item_at = [&](int code, WorkItem& w) {  // code: work code, or -1
         if (code < 0) return false;
         w = decode_item(code >> 2, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
-        if ((code & 3) == 1) {
-            w.rows = kPkBM / 2;
-        } else if ((code & 3) == 2) {
-            w.row_begin += kPkBM / 2;
-            w.rows -= kPkBM / 2;
-        }
+        tail_part(code & 3, kPkBM, w.row_begin, w.rows);
         return true;
     };
     auto item_of_off = [&](int off) {  // work code at offset off of this XCD's work, or -1
@@ -438,7 +434,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         bool split = false;
         if (lane < n_tail) {
             const WorkItem w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
-            split = w.rows > 3 * kPkBM / 4;
+            split = tail_splits(w.rows, kPkBM);
         }
         const uint64_t sb = __ballot(split);
         const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (kWave - lane));

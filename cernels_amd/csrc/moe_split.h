@@ -1,4 +1,5 @@
-// Per-XCD item ranges of the packed grouped GEMMs, balanced by estimated cost. Host and device
+// Per-XCD item ranges of the packed grouped GEMMs, balanced by estimated cost, and the halves their
+// ranges end on (tail_items, below). Host and device
 // code: the route kernel evaluates it per expert, and a CPU test checks it against a brute-force
 // count over the item list (compiled there with CMOE_HD defined empty).
 //
@@ -65,6 +66,28 @@ CMOE_HD inline void split_clamp(int* b, int total, int slots) {
         b[k] = v > b[k - 1] ? v : b[k - 1];
     }
     b[8] = total;
+}
+
+// The tail of one XCD's item range (the packed gate_up GEMM): where the range holds at least three rounds of items
+// for its slots, its last min(tail, max_tail, n_items - 2 slots) items are handed out as two halves when they
+// have more than 3/4 bm rows. The first two offsets of every slot (taken before the tail table exists) are
+// therefore always whole items. A work code is 4 * item + h: h = 0 the whole item, 1 its rows [0, bm/2), 2 its
+// rows [bm/2, rows).
+CMOE_HD inline int tail_items(int n_items, int slots, int tail, int max_tail) {
+    if (n_items < 3 * slots) return 0;
+    const int t = tail < max_tail ? tail : max_tail;
+    const int room = n_items - 2 * slots;
+    return t < room ? t : room;
+}
+CMOE_HD inline bool tail_splits(int rows, int bm) { return 4 * rows > 3 * bm; }
+// The rows of part h of an item that starts at row_begin and has rows rows (h = 0 leaves them).
+CMOE_HD inline void tail_part(int h, int bm, int& row_begin, int& rows) {
+    if (h == 1) {
+        rows = bm / 2;
+    } else if (h == 2) {
+        row_begin += bm / 2;
+        rows -= bm / 2;
+    }
 }
 
 }  // namespace cmoe

@@ -147,3 +147,46 @@ def test_floordiv_at_integer_quotients(split_exe):
     text = "".join(f"D {a} {b}\n" for a, b in pairs)
     out = subprocess.run([str(split_exe)], input=text, capture_output=True, text=True, check=True).stdout.split()
     assert [int(v) for v in out] == [a // b for a, b in pairs]
+
+
+def _tail_codes(exe, cases):
+    text = "".join(f"T {len(rows)} {slots} {tail} {bm} " + " ".join(map(str, rows)) + "\n"
+                   for rows, slots, tail, bm in cases)
+    out = subprocess.run([str(exe)], input=text, capture_output=True, text=True, check=True).stdout
+    got, cur = [], []
+    for line in out.strip().splitlines():
+        if line == "END":
+            got.append(cur)
+            cur = []
+        else:
+            cur.append(tuple(map(int, line.split())))
+    return got
+
+
+def test_tail_halves_cover_every_row_once(split_exe):
+    """The gate_up GEMM's tail (moe_split.h tail_items / tail_splits / tail_part): the work codes of one XCD
+    range give every row of every item to exactly one work unit; only ranges of three or more rounds have a
+    tail, the whole items before it cover the first two offsets of every slot, only items of more than 3/4 bm
+    rows are halved, and no half is empty."""
+    rng = np.random.default_rng(5)
+    cases = [([256] * 121, 32, 12, 256), ([256] * 95, 32, 12, 256), ([100] * 200, 32, 12, 256),
+             ([193, 192, 256, 32] * 30, 32, 12, 256), ([256] * 5, 1, 12, 256), ([256] * 40, 8, 64, 256)]
+    for _ in range(200):
+        n = int(rng.integers(1, 400))
+        rows = rng.integers(1, 257, size=n).tolist()
+        cases.append((rows, int(rng.integers(1, 33)), int(rng.integers(0, 20)), 256))
+    halved = 0
+    for (rows, slots, tail, bm), codes in zip(cases, _tail_codes(split_exe, cases)):
+        n = len(rows)
+        n_tail = min(tail, 16, n - 2 * slots) if n >= 3 * slots else 0
+        assert all(h == 0 for _, h, _, _ in codes[:n - n_tail])
+        assert n - n_tail >= (2 * slots if n_tail else 0)
+        covered = [np.zeros(r, np.int32) for r in rows]
+        for item, h, rb, r in codes:
+            assert r > 0 and 0 <= rb and rb + r <= rows[item], (item, h, rb, r)
+            assert h == 0 or 4 * rows[item] > 3 * bm
+            covered[item][rb:rb + r] += 1
+        assert all((c == 1).all() for c in covered)
+        assert [i for i, _, _, _ in codes] == sorted(i for i, _, _, _ in codes)
+        halved += sum(h == 2 for _, h, _, _ in codes)
+    assert halved > 0

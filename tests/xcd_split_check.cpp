@@ -3,7 +3,10 @@
 //   "S E fw n_tiles slots run_0 .. run_{E-1}" -> the 9 bounds, evaluated the way the route kernel
 //     does: exclusive prefixes of pairs and of 256-row M-tiles over experts, split_expert per
 //     expert, then split_clamp;
-//   "D a b" -> split_floordiv(a, b).
+//   "D a b" -> split_floordiv(a, b);
+//   "T n slots tail bm rows_0 .. rows_{n-1}" (the items of one XCD range) -> one line per work offset,
+//     "item h row_begin rows" (row_begin relative to the item), in the order the packed gate_up GEMM hands
+//     them out: the whole items before the tail, then the tail table (items in order, halves in order).
 #include <cstdio>
 #include <vector>
 
@@ -16,6 +19,30 @@ int main() {
             long long a, b;
             if (std::scanf("%lld %lld", &a, &b) != 2) return 1;
             std::printf("%d\n", cmoe::split_floordiv(a, b));
+            continue;
+        }
+        if (op == 'T') {
+            int n, slots, tail, bm;
+            if (std::scanf("%d %d %d %d", &n, &slots, &tail, &bm) != 4) return 1;
+            std::vector<int> rows(n);
+            for (auto& r : rows) std::scanf("%d", &r);
+            const int n_tail = cmoe::tail_items(n, slots, tail, 16);
+            std::vector<int> codes;
+            for (int i = 0; i < n - n_tail; ++i) codes.push_back(4 * i);
+            for (int i = n - n_tail; i < n; ++i) {
+                if (cmoe::tail_splits(rows[i], bm)) {
+                    codes.push_back(4 * i + 1);
+                    codes.push_back(4 * i + 2);
+                } else {
+                    codes.push_back(4 * i);
+                }
+            }
+            for (int c : codes) {
+                int rb = 0, r = rows[c >> 2];
+                cmoe::tail_part(c & 3, bm, rb, r);
+                std::printf("%d %d %d %d\n", c >> 2, c & 3, rb, r);
+            }
+            std::printf("END\n");
             continue;
         }
         int E, fw, n_tiles, slots;
