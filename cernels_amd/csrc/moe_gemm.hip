@@ -28,11 +28,13 @@
 // neighbours. Workgroup b runs on XCD b % 8; item range [x*per, (x+1)*per) is given to XCD x so
 // that neighbours share that XCD's L2 and each weight tile is fetched from HBM about once.
 //
-// Tile: 128 rows x 128 B-rows x 64 K per step, 256 threads = 4 waves (2 x 2), each wave a
-// 64 x 64 block of v_mfma_f32_32x32x16_bf16. A and B tiles are staged through LDS with a
-// 16-byte chunks XOR-swizzled against LDS bank conflicts (see lds_off).
-// GEMM1's B tile holds 64 gate rows then the 64 matching up rows, so one lane owns the gate and
-// the up value of the same output column and the SwiGLU happens in registers.
+// Two kernels: the concat layout (weights K-contiguous) runs moe_gemm_v3_kernel (128 x 256 tiles,
+// 8 waves, operands copied HBM -> LDS directly); the interleaved gpt-oss layout (weights N-contiguous)
+// runs moe_gemm_kernel: 128 rows x 128 B-rows x 64 K per step, 256 threads = 4 waves (2 x 2), each
+// wave a 64 x 64 block of v_mfma_f32_32x32x16_bf16, B loaded to registers and transposed on its way
+// into LDS. Both stage tiles in LDS as 16-byte chunks XOR-swizzled against bank conflicts (lds_off).
+// GEMM1's B tile holds gate rows then the matching up rows, so one lane owns the gate and the up
+// value of the same output column and the SwiGLU happens in registers.
 #include "moe_tile.h"
 
 namespace cmoe {
@@ -97,14 +99,17 @@ __device__ __forceinline__ void transpose_4x8(const u32x4 (&v)[4], u32x2 (&o)[8]
 // ---- concat-layout grouped GEMM: 128 x 256 tiles, 8 waves, 3-stage direct-to-LDS pipeline ------
 //
 // Weights in the concat layout are K-contiguous ([rows, K]), like the activations, so both operands
-// stream HBM -> LDS with global_load_lds_dwordx4 in the swizzled row layout of lds_off, three
-// k-steps deep (two in flight while the oldest is consumed). 512 threads = 8 waves = two per SIMD,
-// arranged 2 (M) x 4 (N); each wave owns a 64 x 64 block of v_mfma_f32_32x32x16_bf16 results.
+// stream HBM -> LDS with global_load_lds_dwordx4 in the swizzled row layout of lds_off. GEMM1 keeps
+// three 48 KB stages (two in flight while the oldest is consumed); a GEMM2 stage holds the hi and
+// the lo tile of one 64-wide glu chunk beside its weight tile (64 KB), two stages deep. 512 threads =
+// 8 waves = two per SIMD, arranged 2 (M) x 4 (N); each wave owns a 64 x 64 block of
+// v_mfma_f32_32x32x16_bf16 results.
 //   GEMM1 (gate_up): the 256 B-rows are 128 gate rows then the 128 matching up rows, so a wave's
 //     two 32-column blocks are the gate and the up value of the same 32 glu columns.
 //   GEMM2 (down): the 256 B-rows are 256 consecutive output columns.
 // Epilogue: the accumulators go through LDS (the pipeline buffers are free by then) so that every
-// row leaves as contiguous 16-byte stores: 256 B of bf16 glu per row, 1 KB of fp32 per output row.
+// row leaves as contiguous 16-byte stores: 2 x 256 B of bf16 glu (hi, lo) per row, 1 KB of fp32 per
+// output row.
 constexpr int kV3BM = 128;
 constexpr int kV3BN = 256;
 constexpr int kV3Threads = 512;
