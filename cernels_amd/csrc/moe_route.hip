@@ -292,13 +292,16 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_count_scan_kernel(
     if (sched && tid < kSchedInts) sched[tid] = 0;
 }
 
-// The whole route in one launch: workgroup b (1024 threads) owns route tile b. Every workgroup
+// The whole route in one launch: workgroup b < ntiles (1024 threads) owns route tile b. Every workgroup
 // builds all tiles' expert histograms in LDS and scans them (the same work as
 // moe_route_count_scan_kernel, repeated per workgroup: idx is small and L2-resident), which gives it
-// the absolute first write position of each expert in its own tile; workgroup 0 also writes the
-// offsets, tile list and counters. Then each of its 16 waves takes 64 consecutive pairs of the tile:
-// per-wave histograms give the write cursors, and lanes that share an expert are ranked with a
-// bit-sliced ballot, exactly as in the scatter kernel. Output identical to the two-launch route.
+// the absolute first write position of each expert in its own tile. Then each of its 16 waves takes 64
+// consecutive pairs of the tile: per-wave histograms give the write cursors, and lanes that share an
+// expert are ranked with a bit-sliced ballot, exactly as in the scatter kernel. One more workgroup
+// (b = ntiles) writes the offsets, the tile list, the GEMMs' XCD split and counters from the same scans
+// and scatters nothing, so those writes run beside the scatter instead of after it in one workgroup
+// (measured: the workgroup that did both ended the launch ~2.5 us after the others). Output identical
+// to the two-launch route.
 constexpr int kRtChunks = 8;           // 16-byte idx chunks per thread and round of the histogram pass
 constexpr int kRtOneCells = 39 * 1024;  // LDS cells: ntiles * E histograms + 16 * E wave cursors (156 KiB)
 
@@ -313,6 +316,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     __shared__ int wave_tot[kRouteWaves];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), P = T * K;
     const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const bool writer = blockIdx.x == (unsigned)ntiles;  // offsets, tile list, split; owns no tile
     const float rT = 1.0f / (float)T;
     for (int i = tid; i < (ntiles + kRouteWaves) * E; i += kRouteThreads) rt_lds[i] = 0;
     const int q = blockIdx.x * kRtTile + w * kWave + lane;
@@ -362,8 +366,8 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
     const int off = block_exclusive_scan(run, wave_tot, &valid_total);
     const int nt = ceil_div(run, BM);
     const int toff = block_exclusive_scan(nt, wave_tot, &tiles_total);
-    if (blockIdx.x == 0 && split.bounds) write_xcd_split(split, BM, run, nt, off, toff, valid_total, tiles_total, s_split);
-    if (blockIdx.x == 0) {
+    if (writer) {  // uniform over the workgroup (write_xcd_split synchronises it)
+        if (split.bounds) write_xcd_split(split, BM, run, nt, off, toff, valid_total, tiles_total, s_split);
         if (e < E) {
             offsets[e] = off;
             tile_offsets[e] = toff;
@@ -376,6 +380,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_one_kernel(
             meta[1] = valid_total;
         }
         if (sched && tid < kSchedInts) sched[tid] = 0;
+        return;
     }
     if (e < E) {
         int cur = off + mine;
@@ -422,7 +427,7 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
             if (st != hipSuccess) return st;
             lds_attr = true;
         }
-        hipLaunchKernelGGL(moe_route_one_kernel, dim3(nt), dim3(kRouteThreads),
+        hipLaunchKernelGGL(moe_route_one_kernel, dim3(nt + 1), dim3(kRouteThreads),
                            (size_t)(nt + kRouteWaves) * E * sizeof(int32_t), stream, idx, T, K, E, BM, nt, offsets,
                            sorted_pairs, tile_offsets, tile_expert, meta, sched, row_zero, sp);
         return hipGetLastError();
