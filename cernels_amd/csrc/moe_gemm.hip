@@ -28,21 +28,15 @@
 // neighbours. Workgroup b runs on XCD b % 8; item range [x*per, (x+1)*per) is given to XCD x so
 // that neighbours share that XCD's L2 and each weight tile is fetched from HBM about once.
 //
-// Two kernels: the concat layout (weights K-contiguous) runs moe_gemm_v3_kernel (128 x 256 tiles,
-// 8 waves, operands copied HBM -> LDS directly); the interleaved gpt-oss layout (weights N-contiguous)
-// runs moe_gemm_kernel: 128 rows x 128 B-rows x 64 K per step, 256 threads = 4 waves (2 x 2), each
-// wave a 64 x 64 block of v_mfma_f32_32x32x16_bf16, B loaded to registers and transposed on its way
-// into LDS. Both stage tiles in LDS as 16-byte chunks XOR-swizzled against bank conflicts (lds_off).
-// GEMM1's B tile holds gate rows then the matching up rows, so one lane owns the gate and the up
-// value of the same output column and the SwiGLU happens in registers.
+// One tile kernel for both weight layouts (moe_gemm_v3_kernel: 128 x 256 tiles, 8 waves, both operands
+// copied HBM -> LDS directly). The concat layout's weights are K-contiguous and are read like the
+// activations; the interleaved gpt-oss layout's weights are N-contiguous and stay so in LDS, where
+// ds_read_b64_tr_b16 hands each lane the 8 consecutive k of its column (b_frag_nc).
 #include "moe_tile.h"
 
 namespace cmoe {
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;  // B-tile rows (GEMM1: 64 gate + 64 up -> 64 glu columns)
-constexpr int kGemmThreads = 256;
-constexpr int kTileBytes = kBM * kBK * 2;  // 16 KB, A and B alike
+constexpr int kBM = 128;  // rows of an M-tile (the route's tile list is built for it)
 
 // Kernel modes.
 constexpr int kModeGateUp = 0;
@@ -78,35 +72,20 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t& hi, uint16_t& lo) 
 // Offset of glu column n's hi value in a glu row of the pair layout (its lo value is 64 further).
 __device__ __forceinline__ int glu_pair_col(int n) { return 128 * (n >> 6) + (n & 63); }
 
-__device__ __forceinline__ u32x4 ld_global_16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
-
-// Transposes 4 K-rows x 8 columns of bf16 (v[i] = row i) into 8 columns x 4 K (two dwords each).
-__device__ __forceinline__ void transpose_4x8(const u32x4 (&v)[4], u32x2 (&o)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int d = j >> 1;
-        uint32_t a0 = v[0][d], a1 = v[1][d], a2 = v[2][d], a3 = v[3][d];
-        if (j & 1) {
-            o[j][0] = (a0 >> 16) | (a1 & 0xffff0000u);
-            o[j][1] = (a2 >> 16) | (a3 & 0xffff0000u);
-        } else {
-            o[j][0] = (a0 & 0xffffu) | (a1 << 16);
-            o[j][1] = (a2 & 0xffffu) | (a3 << 16);
-        }
-    }
-}
-
-// ---- concat-layout grouped GEMM: 128 x 256 tiles, 8 waves, 3-stage direct-to-LDS pipeline ------
+// ---- grouped GEMM: 128 x 256 tiles, 8 waves, direct-to-LDS pipeline ------------------------------
 //
-// Weights in the concat layout are K-contiguous ([rows, K]), like the activations, so both operands
-// stream HBM -> LDS with global_load_lds_dwordx4 in the swizzled row layout of lds_off. GEMM1 keeps
+// Both operands stream HBM -> LDS with global_load_lds_dwordx4: the activations (and concat weights,
+// K-contiguous [rows, K]) in the swizzled row layout of lds_off, interleaved weights ([K, N]) in the
+// N-contiguous layout of nc_off. GEMM1 keeps
 // three 48 KB stages (two in flight while the oldest is consumed); a GEMM2 stage holds the hi and
 // the lo tile of one 64-wide glu chunk beside its weight tile (64 KB), two stages deep. 512 threads =
 // 8 waves = two per SIMD, arranged 2 (M) x 4 (N); each wave owns a 64 x 64 block of
 // v_mfma_f32_32x32x16_bf16 results.
-//   GEMM1 (gate_up): the 256 B-rows are 128 gate rows then the 128 matching up rows, so a wave's
-//     two 32-column blocks are the gate and the up value of the same 32 glu columns.
-//   GEMM2 (down): the 256 B-rows are 256 consecutive output columns.
+//   GEMM1 (gate_up), concat: the 256 B-rows are 128 gate rows then the 128 matching up rows, so a
+//     wave's two 32-column blocks are the gate and the up value of the same 32 glu columns.
+//   GEMM1, interleaved: the 256 B-columns are 128 (gate, up) column pairs as stored; a lane holds a
+//     gate and its neighbour lane the matching up, paired in the epilogue by a lane exchange.
+//   GEMM2 (down): the 256 B-rows (concat) or B-columns (interleaved) are 256 consecutive output columns.
 // Epilogue: the accumulators go through LDS (the pipeline buffers are free by then) so that every
 // row leaves as contiguous 16-byte stores: 2 x 256 B of bf16 glu (hi, lo) per row, 1 KB of fp32 per
 // output row.
@@ -127,9 +106,33 @@ static_assert(2 * (2 * kV3ABytes + kV3BBytes) <= kV3Lds, "GEMM2 stages fit the a
 constexpr int kV3YStride = kV3BN + 4;              // fp32 epilogue row stride (bank offset per row)
 constexpr int kV3GStride = kV3BN / 2 + 8;          // bf16 epilogue row stride
 
-template <int MODE, int ACT, bool HAS_BIAS>
+// The B tile of the interleaved layout keeps the weights' own [K][N] order (N-contiguous rows of 256
+// columns, 512 bytes); 16-byte chunk q of k-row r sits at chunk q ^ (4 (r % 4)), so the four k-rows and
+// four chunks one half-wave's transposed reads touch fall on distinct banks.
+__device__ __forceinline__ int nc_off(int row, int col) {
+    return row * (kV3BN * 2) + (((col >> 3) ^ (4 * (row & 3))) << 4) + ((col & 7) << 1);
+}
+
+// B operand of v_mfma_f32_32x32x16_bf16 (lane l: k = kb + 8 (l / 32) + 0..7, column cb + l % 32) from an
+// N-contiguous tile, by two ds_read_b64_tr_b16. Within each 16-lane group the lanes' 8-byte rows form a
+// 16 x 4 matrix S of 16-bit values and lane i receives S[4r + i/4][i%4], r = 0..3; so lane i' of a group
+// reading row k0 + i'/4 at column c0 + 4 (i' % 4) receives k-rows k0..k0+3 of column c0 + i'.
+__device__ __forceinline__ bf16x8 b_frag_nc(const unsigned char* sB, int kb, int cb, int lane) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    const int g = lane >> 4, i = lane & 15;
+    const int row = kb + 8 * (g >> 1) + (i >> 2), col = cb + 16 * (g & 1) + 4 * (i & 3);
+    auto rd = [&](int r) {
+        return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(lds_u32(sB) + nc_off(r, col)));
+    };
+    const v4i16 lo = rd(row), hi = rd(row + 4);
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
 __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams prm) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr bool kNc = LAYOUT == kLayoutInterleaved;  // weights N-contiguous: B tile [64 k][256 n]
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int wm = wave & 1, wn = wave >> 1;
@@ -168,15 +171,26 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
         }
 #pragma unroll
         for (int i = 0; i < kV3BPer; ++i) {
-            const int r = 8 * (i * kV3Waves + wave) + lrow;
-            int wrow;
-            if constexpr (MODE == kModeGateUp) {
-                const int c = min(n0 + (r & (halfN - 1)), prm.F - 1);
-                wrow = r < halfN ? c : prm.F + c;
+            if constexpr (kNc) {
+                // copy i of this wave: k-rows 2c and 2c+1 (c = i*8 + wave), 32 chunks of 8 columns each; the chunk
+                // a lane writes (its LDS position) is loaded from chunk position ^ 4 (row % 4); columns past the
+                // matrix read a valid column (their results are not stored)
+                const int r = 2 * (i * kV3Waves + wave) + (lane >> 5);
+                const int ncols = MODE == kModeGateUp ? 2 * prm.F : prm.N;
+                const int c0 = MODE == kModeGateUp ? 2 * n0 : n0;
+                const int col = min(c0 + 8 * ((lane & 31) ^ (4 * (r & 3))), ncols - 8);
+                b_src[i] = Be + (long long)r * prm.ldb + col;
             } else {
-                wrow = min(n0 + r, prm.N - 1);
+                const int r = 8 * (i * kV3Waves + wave) + lrow;
+                int wrow;
+                if constexpr (MODE == kModeGateUp) {
+                    const int c = min(n0 + (r & (halfN - 1)), prm.F - 1);
+                    wrow = r < halfN ? c : prm.F + c;
+                } else {
+                    wrow = min(n0 + r, prm.N - 1);
+                }
+                b_src[i] = Be + (long long)wrow * prm.ldb + ((lane & 7) ^ swz(r)) * 8;
             }
-            b_src[i] = Be + (long long)wrow * prm.ldb + ((lane & 7) ^ swz(r)) * 8;
         }
         constexpr int S = v3_stages<MODE>(), AT = v3_a_tiles<MODE>(), SB = v3_stage_bytes<MODE>();
         constexpr int kCopies = AT * kV3APer + kV3BPer;  // copies per wave per stage
@@ -188,7 +202,9 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
                 for (int i = 0; i < kV3APer; ++i)
                     dma16(a_src[i] + kt * AT * kBK + h * kBK, sa + h * kV3ABytes + i * (kV3Waves * 1024));
 #pragma unroll
-            for (int i = 0; i < kV3BPer; ++i) dma16(b_src[i] + kt * kBK, sa + AT * kV3ABytes + i * (kV3Waves * 1024));
+            for (int i = 0; i < kV3BPer; ++i)
+                dma16(b_src[i] + (kNc ? (long long)kt * kBK * prm.ldb : (long long)kt * kBK),
+                      sa + AT * kV3ABytes + i * (kV3Waves * 1024));
         };
 
         f32x16 acc[2][2];
@@ -199,8 +215,10 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
+        // the wave's two 32-column blocks: B-tile rows (concat) or columns (interleaved; for gate_up 32 physical
+        // columns are 16 gate/up pairs)
         int brow[2];
-        if constexpr (MODE == kModeGateUp) {
+        if constexpr (MODE == kModeGateUp && !kNc) {
             brow[0] = wn * 32;
             brow[1] = halfN + wn * 32;
         } else {
@@ -237,8 +255,10 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
                         af[ks][mb][h] =
                             *reinterpret_cast<const bf16x8*>(sA + h * kV3ABytes + lds_off(arow0 + mb * 32, chunk));
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb)
-                    bfr[ks][nb] = *reinterpret_cast<const bf16x8*>(sB + lds_off(brow[nb] + (lane & 31), chunk));
+                for (int nb = 0; nb < 2; ++nb) {
+                    if constexpr (kNc) bfr[ks][nb] = b_frag_nc(sB, 16 * ks, brow[nb], lane);
+                    else bfr[ks][nb] = *reinterpret_cast<const bf16x8*>(sB + lds_off(brow[nb] + (lane & 31), chunk));
+                }
             }
 #pragma unroll
             for (int ks = 0; ks < kBK / 16; ++ks)
@@ -257,23 +277,49 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
         // row 8*(r/4) + 4*(lane/32) + (r%4), column lane & 31.
         if constexpr (MODE == kModeGateUp) {
             uint16_t* stg = reinterpret_cast<uint16_t*>(smem);  // [2][128][kV3GStride]: the hi tile, the lo tile
-            const int c = wn * 32 + (lane & 31);                 // glu column within the tile
-            float bg = 0.f, bu = 0.f;
-            if constexpr (HAS_BIAS) {
-                const int n = min(n0 + c, prm.F - 1);
-                bg = prm.bias[(long long)e * 2 * prm.F + n];
-                bu = prm.bias[(long long)e * 2 * prm.F + prm.F + n];
-            }
+            if constexpr (kNc) {
+                // physical column 2j is gate, 2j + 1 up of glu column j: even lanes hold gates, their odd
+                // neighbours the matching ups
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
+                for (int nb = 0; nb < 2; ++nb) {
+                    const int pc = brow[nb] + (lane & 31);          // physical column within the tile
+                    const int c = (brow[nb] >> 1) + ((lane & 31) >> 1);  // glu column within the tile
+                    float b = 0.f;
+                    if constexpr (HAS_BIAS) b = prm.bias[(long long)e * 2 * prm.F + min(2 * n0 + pc, 2 * prm.F - 1)];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    uint16_t hi, lo;
-                    split_bf16(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu), hi, lo);
-                    stg[row * kV3GStride + c] = hi;
-                    stg[(kV3BM + row) * kV3GStride + c] = lo;
+                    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const float v = acc[mb][nb][r] + b;
+                            const float u = __shfl_xor(v, 1, kWave);
+                            if (!(lane & 1)) {
+                                const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                                uint16_t hi, lo;
+                                split_bf16(swiglu<ACT>(v, u), hi, lo);
+                                stg[row * kV3GStride + c] = hi;
+                                stg[(kV3BM + row) * kV3GStride + c] = lo;
+                            }
+                        }
                 }
+            } else {
+                const int c = wn * 32 + (lane & 31);  // glu column within the tile
+                float bg = 0.f, bu = 0.f;
+                if constexpr (HAS_BIAS) {
+                    const int n = min(n0 + c, prm.F - 1);
+                    bg = prm.bias[(long long)e * 2 * prm.F + n];
+                    bu = prm.bias[(long long)e * 2 * prm.F + prm.F + n];
+                }
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        uint16_t hi, lo;
+                        split_bf16(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu), hi, lo);
+                        stg[row * kV3GStride + c] = hi;
+                        stg[(kV3BM + row) * kV3GStride + c] = lo;
+                    }
+            }
             __syncthreads();
             uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
             constexpr int kChunks = kV3BN / 2 / 8;  // 16-byte chunks per glu row and half (16)
@@ -319,228 +365,6 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
     }
 }
 
-template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
-__global__ __launch_bounds__(kGemmThreads, 2) void moe_gemm_kernel(GemmParams prm) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    // LDS, 16 KB tiles: A buffers 0,1 then B buffers 0,1. GEMM2 (glu pairs): A (hi) buffers 0,1, one B
-    // buffer, A lo buffers 0,1: 80 KB, so two workgroups still fit a CU; the B buffer is rewritten only
-    // after a barrier that ends every wave's reads of it.
-    constexpr bool kPair = MODE == kModeDown;
-    auto ldsA = [&](int buf) { return smem + buf * kTileBytes; };
-    auto ldsB = [&](int buf) { return smem + (2 + (kPair ? 0 : buf)) * kTileBytes; };
-    auto ldsL = [&](int buf) { return smem + (3 + buf) * kTileBytes; };
-
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int wm = wave & 1, wn = wave >> 1;
-    constexpr bool kBNcontig = (LAYOUT == kLayoutInterleaved);
-
-    const int tiles = prm.meta[0];
-    const int total = tiles * prm.n_tiles;
-    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, slots = gridDim.x >> 3;
-    const int per = ceil_div(total, 8);
-    const int it_end = min(total, (xcd + 1) * per);
-
-    for (int it = xcd * per + slot; it < it_end; it += slots) {
-        // ---- item -> (expert, n-tile, m-tile)
-        const int e = prm.tile_expert[it / prm.n_tiles];
-        const int t0 = prm.tile_offsets[e], nt_e = prm.tile_offsets[e + 1] - t0;
-        const int local = it - t0 * prm.n_tiles;
-        const int n_idx = local / nt_e, m_idx = local - n_idx * nt_e;
-        const int seg0 = prm.offsets[e], seg_n = prm.offsets[e + 1] - seg0;
-        const int row_begin = seg0 + m_idx * kBM;
-        const int rows = min(kBM, seg_n - m_idx * kBM);
-        const int n0 = n_idx * (MODE == kModeGateUp ? kBN / 2 : kBN);  // first output column
-        const uint16_t* Be = prm.B + (long long)e * prm.expert_stride;
-        const int Kd = prm.Kdim;
-
-        // ---- per-thread global source pointers for A (4 rows) and B
-        const int ac = tid & 7;
-        const uint16_t* a_src[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = min((tid >> 3) + 32 * i, rows - 1);
-            long long src_row;
-            if constexpr (MODE == kModeGateUp) src_row = prm.sorted_pairs[row_begin + r] / prm.topk;
-            else src_row = row_begin + r;
-            a_src[i] = prm.A + src_row * Kd + ac * 8;
-        }
-        const uint16_t* b_src[4];
-        if constexpr (!kBNcontig) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = (tid >> 3) + 32 * i;  // B-tile row
-                int wrow;
-                if constexpr (MODE == kModeGateUp) {
-                    const int c = min(n0 + (r & 63), prm.F - 1);
-                    wrow = r < 64 ? c : prm.F + c;
-                } else {
-                    wrow = min(n0 + r, prm.N - 1);
-                }
-                b_src[i] = Be + (long long)wrow * prm.ldb + ac * 8;
-            }
-        } else {
-            // 4 K-rows x 8 columns per thread; columns of W [K, ncols]
-            const int ng = tid & 15, kg = tid >> 4;
-            const int ncols = (MODE == kModeGateUp) ? 2 * prm.F : prm.N;
-            int col = (MODE == kModeGateUp ? 2 * n0 : n0) + ng * 8;
-            if (col + 8 > ncols) col = (MODE == kModeGateUp ? 2 * n0 : n0);  // tail: any valid column
-#pragma unroll
-            for (int i = 0; i < 4; ++i) b_src[i] = Be + (long long)(kg * 4 + i) * prm.ldb + col;
-        }
-
-        f32x16 acc[2][2];
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
-
-        constexpr int AT = kPair ? 2 : 1;  // A tiles per stage: glu hi and lo for GEMM2
-        u32x4 ra[AT][4], rb[4];
-        auto load_regs = [&](int kt) {
-#pragma unroll
-            for (int h = 0; h < AT; ++h)  // GEMM2: A columns [128 kt, 128 kt + 64) hi, then the lo half
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ra[h][i] = ld_global_16(a_src[i] + kt * AT * kBK + h * kBK);
-            if constexpr (!kBNcontig) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + kt * kBK);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) rb[i] = ld_global_16(b_src[i] + (long long)kt * kBK * prm.ldb);
-            }
-        };
-        auto store_a = [&](int buf) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                *reinterpret_cast<u32x4*>(ldsA(buf) + lds_off((tid >> 3) + 32 * i, ac)) = ra[0][i];
-                if constexpr (kPair) *reinterpret_cast<u32x4*>(ldsL(buf) + lds_off((tid >> 3) + 32 * i, ac)) = ra[AT - 1][i];
-            }
-        };
-        auto store_b = [&](int buf) {
-            if constexpr (!kBNcontig) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    *reinterpret_cast<u32x4*>(ldsB(buf) + lds_off((tid >> 3) + 32 * i, ac)) = rb[i];
-            } else {
-                u32x2 o[8];
-                transpose_4x8(rb, o);
-                const int ng = tid & 15, kg = tid >> 4;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int nl = ng * 8 + j;
-                    int lrow;
-                    if constexpr (MODE == kModeGateUp) lrow = (nl & 1) ? 64 + (nl >> 1) : (nl >> 1);
-                    else lrow = nl;
-                    *reinterpret_cast<u32x2*>(ldsB(buf) + lds_off(lrow, kg >> 1) + (kg & 1) * 8) = o[j];
-                }
-            }
-        };
-
-        // B-tile rows used by this wave for its two 32-column blocks
-        int brow[2];
-        if constexpr (MODE == kModeGateUp) {
-            brow[0] = wn * 32;       // gate
-            brow[1] = 64 + wn * 32;  // up
-        } else {
-            brow[0] = wn * 64;
-            brow[1] = wn * 64 + 32;
-        }
-        const int arow0 = wm * 64 + (lane & 31);
-        const int khalf = lane >> 5;
-
-        const int nk = Kd / (AT * kBK);  // GEMM2: Kd = 2F, one stage per 64-wide k-chunk of glu
-        load_regs(0);
-        store_a(0);
-        store_b(0);
-        __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-            const int buf = kt & 1;
-            if (kt + 1 < nk) load_regs(kt + 1);
-#pragma unroll
-            for (int ks = 0; ks < kBK / 16; ++ks) {
-                const int chunk = ks * 2 + khalf;
-                bf16x8 af[2][AT], bfr[2];
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    af[mb][0] = *reinterpret_cast<const bf16x8*>(ldsA(buf) + lds_off(arow0 + mb * 32, chunk));
-                    if constexpr (kPair)
-                        af[mb][AT - 1] = *reinterpret_cast<const bf16x8*>(ldsL(buf) + lds_off(arow0 + mb * 32, chunk));
-                }
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb)
-                    bfr[nb] = *reinterpret_cast<const bf16x8*>(ldsB(buf) + lds_off(brow[nb] + (lane & 31), chunk));
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-                        for (int h = 0; h < AT; ++h)
-                            acc[mb][nb] =
-                                __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mb][h], bfr[nb], acc[mb][nb], 0, 0, 0);
-            }
-            if (kt + 1 < nk) {
-                store_a(buf ^ 1);
-                if constexpr (kPair) __syncthreads();  // every wave is done with the one B buffer
-                store_b(buf ^ 1);
-            }
-            __syncthreads();
-        }
-
-        // ---- epilogue. Output lane layout of the 32x32 block: column = lane & 31,
-        // row = 8*(r/4) + 4*(lane/32) + (r%4) for accumulator element r.
-        if constexpr (MODE == kModeGateUp) {
-            uint16_t* glu = reinterpret_cast<uint16_t*>(prm.out);
-            const int n = n0 + wn * 32 + (lane & 31);
-            if (n < prm.N) {
-                float bg = 0.f, bu = 0.f;
-                if constexpr (HAS_BIAS) {
-                    const float* be = prm.bias + (long long)e * 2 * prm.F;
-                    bg = LAYOUT == kLayoutInterleaved ? be[2 * n] : be[n];
-                    bu = LAYOUT == kLayoutInterleaved ? be[2 * n + 1] : be[prm.F + n];
-                }
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        if (row < rows) {
-                            uint16_t hi, lo;
-                            split_bf16(swiglu<ACT>(acc[mb][0][r] + bg, acc[mb][1][r] + bu), hi, lo);
-                            uint16_t* g = glu + (long long)(row_begin + row) * 2 * prm.F + glu_pair_col(n);
-                            g[0] = hi;
-                            g[64] = lo;
-                        }
-                    }
-            }
-        } else {
-            float* Y = reinterpret_cast<float*>(prm.out);
-#pragma unroll
-            for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int row = wm * 64 + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (row < rows) {
-                        const int p = prm.sorted_pairs[row_begin + row];
-                        const float w = prm.route_w[p];
-#pragma unroll
-                        for (int nb = 0; nb < 2; ++nb) {
-                            const int n = n0 + brow[nb] + (lane & 31);
-                            if (n < prm.N) {
-                                float v = acc[mb][nb][r];
-                                if constexpr (HAS_BIAS) v += prm.bias[(long long)e * prm.N + n];
-                                Y[(long long)p * prm.N + n] = v * w;
-                            }
-                        }
-                    }
-                }
-            }
-        }
-        __syncthreads();  // LDS reuse by the next item
-    }
-}
-
 // out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] ), slots in k order.
 // One workgroup per token; a thread owns 8 consecutive columns (two 16-byte loads per slot, one
 // 16-byte store).
@@ -577,41 +401,25 @@ static int cu_count() {
 
 int gemm_tile_m() { return kBM; }
 
-template <int MODE, int ACT, bool HAS_BIAS>
+template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
 static hipError_t launch_v3_t(const GemmParams& prm, int upper, hipStream_t stream) {
     static bool attr = false;
     if (!attr) {
-        hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_v3_kernel<MODE, ACT, HAS_BIAS>,
+        hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_v3_kernel<MODE, LAYOUT, ACT, HAS_BIAS>,
                                             hipFuncAttributeMaxDynamicSharedMemorySize, kV3Lds);
         if (st != hipSuccess) return st;
         attr = true;
     }
     int grid = min(upper, cu_count());
     grid = ceil_div(max(grid, 1), 8) * 8;
-    hipLaunchKernelGGL((moe_gemm_v3_kernel<MODE, ACT, HAS_BIAS>), dim3(grid), dim3(kV3Threads), kV3Lds, stream, prm);
+    hipLaunchKernelGGL((moe_gemm_v3_kernel<MODE, LAYOUT, ACT, HAS_BIAS>), dim3(grid), dim3(kV3Threads), kV3Lds,
+                       stream, prm);
     return hipGetLastError();
 }
 
 template <int MODE, int LAYOUT, int ACT, bool HAS_BIAS>
 static hipError_t launch_gemm_t(const GemmParams& prm, int max_tiles, hipStream_t stream) {
-    const int upper = max_tiles * prm.n_tiles;
-    if constexpr (LAYOUT == kLayoutConcat) {
-        return launch_v3_t<MODE, ACT, HAS_BIAS>(prm, upper, stream);
-    } else {
-        int grid = min(upper, cu_count() * 2);
-        grid = ceil_div(max(grid, 1), 8) * 8;
-        const size_t lds = (MODE == kModeDown ? 5 : 4) * (size_t)kTileBytes;  // 80 KB (glu pairs) or 64 KB
-        static bool attr = false;
-        if (!attr) {  // above 64 KB of dynamic LDS the kernel has to allow it
-            hipError_t st = hipFuncSetAttribute((const void*)moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>,
-                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (st != hipSuccess) return st;
-            attr = true;
-        }
-        hipLaunchKernelGGL((moe_gemm_kernel<MODE, LAYOUT, ACT, HAS_BIAS>), dim3(grid), dim3(kGemmThreads), lds,
-                           stream, prm);
-    }
-    return hipGetLastError();
+    return launch_v3_t<MODE, LAYOUT, ACT, HAS_BIAS>(prm, max_tiles * prm.n_tiles, stream);
 }
 
 hipError_t launch_gateup(const GemmParams& prm, int layout, int act, bool has_bias, int max_tiles, hipStream_t s) {
@@ -680,7 +488,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g1.N = F;
     g1.F = F;
     g1.topk = K;
-    g1.n_tiles = concat ? ceil_div(F, kV3BN / 2) : ceil_div(F, kBN / 2);
+    g1.n_tiles = ceil_div(F, kV3BN / 2);
     g1.expert_stride = 2LL * F * H;
     g1.ldb = concat ? H : 2 * F;
     st = launch_gateup(g1, layout, act, b1 != nullptr, max_tiles, s);
@@ -693,7 +501,7 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     g2.out = Y;
     g2.Kdim = 2 * F;  // the glu pair: 2F bf16 values per row
     g2.N = H;
-    g2.n_tiles = concat ? ceil_div(H, kV3BN) : ceil_div(H, kBN);
+    g2.n_tiles = ceil_div(H, kV3BN);
     g2.expert_stride = (long long)H * F;
     g2.ldb = concat ? F : H;
     st = launch_down(g2, layout, b2 != nullptr, max_tiles, s);
