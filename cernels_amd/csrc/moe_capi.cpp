@@ -274,7 +274,7 @@ int cernels_moe_experts_packed(const void* x, const void* gate_up_packed, const 
 // ---- megablocks_moe: non-gated experts on weights as stored, packed into the workspace per call ----
 
 namespace {
-int megablocks_act(int act_id) {
+static int megablocks_act(int act_id) {
     switch (act_id) {
         case 0: return CERNELS_MOE_ACT_GELU_TANH;
         case 1: return CERNELS_MOE_ACT_SILU_PLAIN;
@@ -285,7 +285,7 @@ int megablocks_act(int act_id) {
 struct MegaWs {
     size_t w1, w2, run, total;
 };
-MegaWs megablocks_ws(int T, int H, int F, int E, int K) {
+static MegaWs megablocks_ws(int T, int H, int F, int E, int K) {
     MegaWs m{};
     m.w1 = 0;
     m.w2 = align_up(cmoe::packed_weight_bytes(H, F, E, CERNELS_MOE_UP));
@@ -332,8 +332,8 @@ size_t cernels_moe_experts_decode_workspace_bytes(int32_t T, int32_t H, int32_t 
 
 namespace {
 // Every check of the decode entry except the workspace's size, in the entry's order.
-int decode_checks(const void* x, const void* w1, const void* w2, const int32_t* idx, const float* wts, int T, int H,
-                  int F, int E, int K, int layout, int act, void* out, const void* ws) {
+static int decode_checks(const void* x, const void* w1, const void* w2, const int32_t* idx, const float* wts, int T,
+                         int H, int F, int E, int K, int layout, int act, void* out, const void* ws) {
     int st = common_checks(x, w1, w2, idx, wts, T, H, F, E, K, layout, act, out, const_cast<void*>(ws));
     if (st != CERNELS_MOE_OK || T == 0) return st;
     if (layout != CERNELS_MOE_LAYOUT_CONCAT || !act_gated(act)) return CERNELS_MOE_UNSUPPORTED_SHAPE;
