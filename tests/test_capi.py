@@ -25,6 +25,21 @@ def test_every_declared_symbol_is_exported(L):
     assert set(names) == set(_native._SIGNATURES), "ctypes signature table out of sync with the header"
 
 
+def test_no_undeclared_c_symbols_are_exported(L):
+    """The library's unmangled (C-linkage) exports are exactly the header's functions: no internal helper
+    leaks into the ABI a binding could come to depend on."""
+    import shutil
+    import subprocess
+
+    if shutil.which("nm") is None:
+        pytest.skip("nm not available")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {parts[2] for parts in (line.split() for line in out.splitlines())
+                if len(parts) == 3 and parts[1] == "T" and not parts[2].startswith("_Z")}
+    assert exported == set(_native.header_functions()), sorted(exported ^ set(_native.header_functions()))
+
+
 def test_version_and_status_strings(L):
     assert b"gfx950" in L.cernels_moe_version()
     for code, text in _native.STATUS.items():
