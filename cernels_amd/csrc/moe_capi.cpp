@@ -72,7 +72,7 @@ PrefillWs prefill_ws(int T, int H, int F, int E, int K) {
     w.tile_expert = o;  o = align_up(o + sizeof(int32_t) * (size_t)(w.capacity > 0 ? w.capacity : 1));
     w.route_counts = o; o = align_up(o + cmoe::route_workspace_bytes(T, K, E));
     w.glu = o;          o = align_up(o + sizeof(uint16_t) * 2 * P * F);  // stored layout: bf16 pairs; packed: fp16
-    w.Y = o;            o = align_up(o + sizeof(float) * P * H);  // fp32 (stored layout) or 24-bit floats (packed)
+    w.Y = o;            o = align_up(o + 3 * P * H);  // 24-bit floats (both paths)
     w.gexp = o;         o = align_up(o + (size_t)P * (F / 16));  // packed path: exponent per 16-column glu segment
     w.rsig = o;         o = align_up(o + (size_t)P);             // packed path: per glu row scale
     w.psig = o;         o = align_up(o + (size_t)P);             // packed path: the same, per pair

@@ -1,9 +1,9 @@
 // Prefill grouped GEMMs for the routed experts, bf16 MFMA on gfx950.
 //
 //   GEMM1  glu[r, :]  = act( X[tok(r), :] · W1_e^T )   rows r of expert e, SwiGLU in the epilogue
-//   GEMM2  Y[p, :]    = w_p · ( glu[r, :] · W2_e^T + b2_e )   fp32, at the pair's own row p
-//   combine out[t, :] = bf16( sum_k Y[t*K + k, :] )   (slots in k order)
-// Y stays fp32: rounding each of the K weighted rows to bf16 before the k-sum costs about
+//   GEMM2  Y[p, :]    = w_p · ( glu[r, :] · W2_e^T + b2_e )   24-bit floats, at the pair's own row p
+//   combine out[t, :] = bf16( sum_k Y[t*K + k, :] )   (slots in k order; moe_combine_h_kernel)
+// Y keeps 16 mantissa bits: rounding each of the K weighted rows to bf16 before the k-sum costs about
 // 0.006*RMS of extra error, more than the 2e-2*RMS budget leaves after the output's own rounding.
 //
 // glu as a bf16 pair. GEMM1 stores each glu value v as hi = bf16(v) and lo = bf16(v - hi); hi + lo
@@ -87,8 +87,8 @@ __device__ __forceinline__ int glu_pair_col(int n) { return 128 * (n >> 6) + (n 
 //     gate and its neighbour lane the matching up, paired in the epilogue by a lane exchange.
 //   GEMM2 (down): the 256 B-rows (concat) or B-columns (interleaved) are 256 consecutive output columns.
 // Epilogue: the accumulators go through LDS (the pipeline buffers are free by then) so that every
-// row leaves as contiguous 16-byte stores: 2 x 256 B of bf16 glu (hi, lo) per row, 1 KB of fp32 per
-// output row.
+// row leaves as contiguous stores: 2 x 256 B of bf16 glu (hi, lo) per row, 768 B of 24-bit Y per output
+// row (12 bytes per four columns).
 constexpr int kV3BM = 128;
 constexpr int kV3BN = 256;
 constexpr int kV3Threads = 512;
@@ -344,8 +344,10 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
                         stg[row * kV3YStride + brow[nb] + (lane & 31)] = acc[mb][nb][r];
                     }
             __syncthreads();
-            float* Y = reinterpret_cast<float*>(prm.out);
-            constexpr int kChunks = kV3BN / 4;  // 16-byte chunks per output row (64)
+            // Y rows in the 24-bit float form (four columns per 12 bytes): the combine sums the K rows of a
+            // token from values rounded at 2^-16, at 3/4 of fp32's bytes
+            unsigned char* Yb = reinterpret_cast<unsigned char*>(prm.out);
+            constexpr int kChunks = kV3BN / 4;  // four-column groups per output row (64)
             for (int i = tid; i < kV3BM * kChunks; i += kV3Threads) {
                 const int row = i / kChunks, ch = i - row * kChunks;
                 const int n = n0 + ch * 4;
@@ -357,7 +359,9 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
                         const f32x4 b = *reinterpret_cast<const f32x4*>(prm.bias + (long long)e * prm.N + n);
                         v += b;
                     }
-                    *reinterpret_cast<f32x4*>(Y + (long long)p * prm.N + n) = v * w;
+                    v *= w;
+                    const f24x4 q = pack_f24x4(v[0], v[1], v[2], v[3]);
+                    __builtin_memcpy(Yb + ((long long)p * prm.N + n) * 3, &q, 12);
                 }
             }
         }
@@ -365,25 +369,6 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
     }
 }
 
-// out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] ), slots in k order.
-// One workgroup per token; a thread owns 8 consecutive columns (two 16-byte loads per slot, one
-// 16-byte store).
-__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ Y, const int32_t* __restrict__ idx,
-                                                          uint16_t* __restrict__ out, int T, int K, int E, int H) {
-    const int t = blockIdx.x;
-    for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < K; ++k) {
-            const int e = idx[t * K + k];
-            if ((unsigned)e >= (unsigned)E) continue;
-            const float* y = Y + ((long long)t * K + k) * H + 8 * c;
-            s0 += *reinterpret_cast<const f32x4*>(y);
-            s1 += *reinterpret_cast<const f32x4*>(y + 4);
-        }
-        *reinterpret_cast<u32x4*>(out + (long long)t * H + 8 * c) =
-            u32x4{pack_bf16x2(s0[0], s0[1]), pack_bf16x2(s0[2], s0[3]), pack_bf16x2(s1[0], s1[1]), pack_bf16x2(s1[2], s1[3])};
-    }
-}
 
 static int g_cu_count = 0;
 
@@ -445,12 +430,9 @@ hipError_t launch_down(const GemmParams& prm, int layout, bool has_bias, int max
                     : launch_gemm_t<kModeDown, kLayoutInterleaved, kActSilu, false>(prm, max_tiles, s);
 }
 
-hipError_t launch_combine(const float* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
-                          hipStream_t s) {
-    if (T == 0) return hipSuccess;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, s, Y, idx, out, T, K, E, H);
-    return hipGetLastError();
-}
+hipError_t launch_combine_h(const unsigned char* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
+                            const int32_t* sync, const int8_t* psig, const float* b2, const float* route_w,
+                            hipStream_t s);
 
 hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t* offsets, int32_t* sorted_pairs,
                         int32_t* tile_offsets, int32_t* tile_expert, int32_t* meta, int32_t* counts,
@@ -507,7 +489,9 @@ hipError_t launch_prefill(const void* x, const void* w1, const float* b1, const 
     st = launch_down(g2, layout, b2 != nullptr, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(3);
-    st = launch_combine(Y, idx, static_cast<uint16_t*>(out), T, K, E, H, s);
+    // Y already holds w (glu W2 + b2): the combine adds no bias and reads no glu scale
+    st = launch_combine_h(reinterpret_cast<const unsigned char*>(Y), idx, static_cast<uint16_t*>(out), T, K, E, H,
+                          nullptr, nullptr, nullptr, route_w, s);
     mark(4);
     return st;
 }

@@ -816,10 +816,11 @@ hipError_t launch_route(const int32_t* idx, int T, int K, int E, int BM, int32_t
                         int32_t* sched, hipStream_t stream, int8_t* row_zero = nullptr,
                         const XcdSplit* split = nullptr);
 // out[t, :] = bf16( sum over valid slots k of Y[t*K + k, :] * 2^psig + w[t, k] * b2[e] ), slots in k
-// order, Y in the 24-bit float form the packed down GEMM writes (w * glu W2, without the bias; psig only
-// when some glu row was stored scaled). One workgroup per token, H/8 threads rounded up to whole waves;
-// a thread owns 8 consecutive columns (two 12-byte loads per slot) and issues the loads of four slots
-// before it adds them, still in slot order.
+// order, Y in the 24-bit float form both down GEMMs write (the packed one: w * glu W2, without the bias;
+// psig only when some glu row was stored scaled, i.e. sync non-null and sync[1] set; the stored-layout one:
+// w * (glu W2 + b2), with bias and sync null). One workgroup per token, H/8 threads rounded up to whole
+// waves; a thread owns 8 consecutive columns (two 12-byte loads per slot) and issues the loads of four
+// slots before it adds them, still in slot order.
 __global__ __launch_bounds__(1024) void moe_combine_h_kernel(const unsigned char* __restrict__ Yb,
                                                             const int32_t* __restrict__ idx, uint16_t* __restrict__ out,
                                                             int T, int K, int E, int H,
@@ -827,7 +828,7 @@ __global__ __launch_bounds__(1024) void moe_combine_h_kernel(const unsigned char
                                                             const int8_t* __restrict__ psig,
                                                             const float* __restrict__ bias, const float* __restrict__ route_w) {
     const int t = blockIdx.x;
-    const bool scaled = sync[1] != 0;  // some glu row was stored scaled: its Y row is scaled by 2^-psig
+    const bool scaled = sync != nullptr && sync[1] != 0;  // some glu row was stored scaled: its Y row is scaled by 2^-psig
     for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
         f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
         for (int k0 = 0; k0 < K; k0 += 4) {
@@ -931,6 +932,10 @@ static int pick_fw(long long P, int E, int NF, int Kd, int cus) {
     return best_w;
 }
 
+hipError_t launch_combine_h(const unsigned char* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
+                            const int32_t* sync, const int8_t* psig, const float* b2, const float* route_w,
+                            hipStream_t s);
+
 // route -> packed gate_up GEMM -> packed down GEMM -> combine, all on stream s. Shapes were checked
 // by the caller (H % 64 == 0, F % 64 == 0, E <= 1024, T >= 1).
 hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1, const void* w2p, const float* b2,
@@ -1022,12 +1027,19 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     st = launch_pk_t<kModePkDown, kActSilu, false>(g2, max_tiles, s);
     if (st != hipSuccess) return st;
     mark(3);
-    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(std::min(1024, ceil_div(H / 8, kWave) * kWave)), 0, s,
-                       reinterpret_cast<const unsigned char*>(Y), idx, static_cast<uint16_t*>(out), T, K, E, H, meta + 24,
-                       psig, b2, route_w);
-    st = hipGetLastError();
+    st = launch_combine_h(reinterpret_cast<const unsigned char*>(Y), idx, static_cast<uint16_t*>(out), T, K, E, H,
+                          meta + 24, psig, b2, route_w, s);
     mark(4);
     return st;
+}
+
+hipError_t launch_combine_h(const unsigned char* Y, const int32_t* idx, uint16_t* out, int T, int K, int E, int H,
+                            const int32_t* sync, const int8_t* psig, const float* b2, const float* route_w,
+                            hipStream_t s) {
+    if (T == 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_combine_h_kernel, dim3(T), dim3(std::min(1024, ceil_div(H / 8, kWave) * kWave)), 0, s, Y,
+                       idx, out, T, K, E, H, sync, psig, b2, route_w);
+    return hipGetLastError();
 }
 
 }  // namespace cmoe
