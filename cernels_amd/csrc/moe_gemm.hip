@@ -76,11 +76,10 @@ __device__ __forceinline__ int glu_pair_col(int n) { return 128 * (n >> 6) + (n 
 //
 // Both operands stream HBM -> LDS with global_load_lds_dwordx4: the activations (and concat weights,
 // K-contiguous [rows, K]) in the swizzled row layout of lds_off, interleaved weights ([K, N]) in the
-// N-contiguous layout of nc_off. GEMM1 keeps
-// three 48 KB stages (two in flight while the oldest is consumed); a GEMM2 stage holds the hi and
-// the lo tile of one 64-wide glu chunk beside its weight tile (64 KB), two stages deep. 512 threads =
-// 8 waves = two per SIMD, arranged 2 (M) x 4 (N); each wave owns a 64 x 64 block of
-// v_mfma_f32_32x32x16_bf16 results.
+// N-contiguous layout of nc_off. GEMM1 keeps three 48 KB stages (two in flight while the oldest is
+// consumed); a GEMM2 stage holds the hi and the lo tile of one 64-wide glu chunk beside its weight tile
+// (64 KB), two stages deep. 512 threads = 8 waves = two per SIMD, arranged 2 (M) x 4 (N); each wave owns
+// a 64 x 64 block of v_mfma_f32_32x32x16_bf16 results.
 //   GEMM1 (gate_up), concat: the 256 B-rows are 128 gate rows then the 128 matching up rows, so a
 //     wave's two 32-column blocks are the gate and the up value of the same 32 glu columns.
 //   GEMM1, interleaved: the 256 B-columns are 128 (gate, up) column pairs as stored; a lane holds a
