@@ -9,17 +9,17 @@
 // each 32x16 MFMA operand fragment is 1 KB of contiguous memory in exactly the order a wave's lanes
 // consume it. A wave streams its weight columns straight into registers with one contiguous 1 KB
 // read per fragment: nothing of the weights goes through LDS. Only the activation tile (token rows
-// gathered through the expert-sorted pair list) is staged in LDS, where all eight waves of the
-// workgroup read it.
+// gathered through the expert-sorted pair list) goes to LDS, copied there directly from global memory
+// (buffer_load ... lds, no registers), where all eight waves of the workgroup read it.
 //
 // Workgroup: 8 waves (two per SIMD), one workgroup per CU, items of 256 rows x 8 fragments. Each
 // wave owns one 32-column weight fragment for all 256 rows of the item (eight 32x32 accumulator
 // blocks), so a weight fragment is fetched once per item and feeds 8 MFMAs, and the activation tile
 // is fetched once per item and feeds 8 fragments. The CU's vector-memory pipe (address and data
-// units, L1) carries 8 KB per 32 MFMAs of a wave, which is what bounds this kernel at these shapes,
-// not HBM. Blocks past the item's rows are skipped (the k-loop is instantiated per block count).
-// K advances in stages of 64: weight loads are issued two stages, activation loads one stage
-// before their MFMAs.
+// units, L1) carries 8 KB per 32 MFMAs of a wave, and with it the L2 misses of the weight stream,
+// which is what bounds this kernel at these shapes. Blocks past the item's rows are skipped (the
+// k-loop is instantiated per block count). K advances in stages of 64 held in three LDS buffers and
+// three weight register slots: both operands of a stage are requested two stages before its MFMAs.
 //
 // GEMM1 fragments hold 16 gate and the 16 matching up columns, so one wave holds both inputs of the
 // gated activation for its 16 glu columns; a v_permlane16_swap pairs them up in the epilogue.
@@ -244,19 +244,23 @@ template <int N>
 using IC = std::integral_constant<int, N>;
 
 // MODE/ACT/HAS_BIAS select the projection; XPF: the reduction has at least two stages, and the
-// next item's first stages are loaded during the current item's last two steps (cross-item
-// prefetch); ODD: the number of stages is odd, so consecutive items alternate the parity of their
-// LDS buffer and weight register slot.
-template <int MODE, int ACT, bool HAS_BIAS, bool XPF, bool ODD>
+// next item's first two stages are copied and loaded during the current item's last two steps
+// (cross-item prefetch); R3: the number of stages mod 3, which sets the k-loop's empty positions.
+template <int MODE, int ACT, bool HAS_BIAS, bool XPF, int R3>
 __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams prm) {
-    static_assert(XPF || ODD, "a single-stage reduction is odd");
+    static_assert(XPF || R3 == 1, "without prefetch the reduction is one stage");
     static_assert(MODE != kModePkUp || !HAS_BIAS, "the non-gated projection has no bias");
     static_assert(MODE != kModePkDown || !HAS_BIAS, "the down bias is added by the combine");
     // GEMM2 multiplies fp16 glu by fp16 weights; the first projections bf16 x by bf16 weights.
     using OpT = std::conditional_t<MODE == kModePkDown, f16x8, bf16x8>;
     // the first projection gathers token rows of x through the pair list; down reads its own glu rows
     constexpr bool kGather = MODE != kModePkDown;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[2 * kPkABytes];
+    // The activation stages: three LDS buffers, declared as separate arrays so that the compiler tells
+    // a copy into one from a read of another (its wait before a read then covers only the copies into
+    // that buffer).
+    __shared__ __attribute__((aligned(16))) unsigned char sA0[kPkABytes];
+    __shared__ __attribute__((aligned(16))) unsigned char sA1[kPkABytes];
+    __shared__ __attribute__((aligned(16))) unsigned char sA2[kPkABytes];
     // Epilogue tables, double-buffered by item parity: row -> pair and routing weight (GEMM2), and
     // the N-tile's bias (GEMM1: 128 gate then 128 up entries; GEMM2: 256 columns).
     __shared__ int s_pair[2][kPkBM];
@@ -279,7 +283,10 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         b_hi = min(b_lo + per, total);
     }
     const int Kd = prm.Kd, nst = Kd / kBK;
-    const int a_chunk = tid & 7;
+    // A copy instruction puts lane l's 16 bytes at LDS position l of the wave's 1 KB (8 rows of the
+    // tile), i.e. at chunk position tid & 7 of its row; in the swizzled layout (lds_off) that position
+    // holds chunk (tid & 7) ^ swz(row), and swz(row) = (tid >> 4) & 7 for every row the thread copies.
+    const int a_chunk = (tid & 7) ^ ((tid >> 4) & 7);
 
     // Items of XCD x are one contiguous range of the list, [bounds[x], bounds[x+1]) (moe_split.h: of
     // about equal estimated cost where workgroups run many items, else equal in count), so that the items that share
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         if (off < n_whole) return 4 * (b_lo + off);
         if (n_tail == 0) return -1;
         const int t = off - n_whole;
-        return t < s_ntail ? s_tail[t] : -1;
+        return __builtin_amdgcn_readfirstlane(t < s_ntail ? s_tail[t] : -1);  // uniform: a work code from LDS
     };
     __shared__ int s_next;  // work code of the item after next (or -1), published once per item
     // Operands are read with buffer loads: a 128-bit descriptor per operand and item (uniform,
@@ -384,22 +391,47 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const uint32_t b_lane = (uint32_t)lane * 16u;
 
     f32x16 acc[kPkMB];
-    u32x4 areg[kPkMB / 2];  // activation chunks of the next stage
-    u32x4 breg[2][4];       // weight fragments: slot d holds the four k-steps of one stage
-    auto a_ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t ao, int stage) {
-        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, ao, stage * kBK * 2, 0));
+    u32x4 breg[3][4];  // weight fragments: slot d holds the four k-steps of one stage
+    auto sbuf = [&](auto bc) -> unsigned char* {
+        constexpr int b = decltype(bc)::value;
+        if constexpr (b == 0) return sA0;
+        else if constexpr (b == 1) return sA1;
+        else return sA2;
+    };
+    // The same buffer as an LDS-address-space pointer (the cast of the array itself folds away).
+    using lds_bytes = __attribute__((address_space(3))) unsigned char*;
+    auto sbuf_lds = [&](auto bc) { return (lds_bytes)sbuf(bc); };
+    // Activation chunk i of this thread (tile row 64 i + tid / 8) of stage `stage`, copied from global
+    // memory straight into LDS buffer b (no registers): 16 bytes per lane, the wave's 64 lanes fill the
+    // 1 KB of rows 64 i + 8 wave .. 64 i + 8 wave + 7.
+    auto copy_a = [&](__amdgpu_buffer_rsrc_t r, uint32_t ao, int stage, auto bc, int i) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (__attribute__((address_space(3))) void*)(sbuf_lds(bc) + (64 * i + 8 * wave) * kBK * 2), 16, ao,
+            stage * kBK * 2, 0, 0);
     };
     auto b_ld = [&](__amdgpu_buffer_rsrc_t r, int bs, int stage, int q) {
         return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, b_lane, (4 * stage + q) * bs, 0));
     };
-    auto store_a = [&](auto nc, auto bc) {  // the first n loaded activation chunks -> LDS buffer b
-        constexpr int n = decltype(nc)::value, b = decltype(bc)::value;
-        unsigned char* sA = smem + b * kPkABytes;
-#pragma unroll
-        for (int i = 0; i < n; ++i) *reinterpret_cast<u32x4*>(sA + lds_off((tid >> 3) + 64 * i, a_chunk)) = areg[i];
+    // Step barrier of a stage in buffer b. The read of buffer b makes the compiler wait for this wave's
+    // copies into b (and only those: the buffers are separate arrays); after the barrier every wave's
+    // copies into b have landed. There is no fence: a workgroup fence would wait for every copy in flight.
+    auto stage_barrier = [&](auto bc) {
+        asm volatile("" ::: "memory");
+        const uint32_t v = *(volatile __attribute__((address_space(3))) const uint32_t*)sbuf_lds(bc);
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        return v;  // consumed at the end of the step, so that its register is not reused (and waited for) early
     };
-    // The whole set-up of one item without prefetch: offsets, tables into buffer tb, stage 0 into
-    // LDS buffer 0, weight stages 0 and 1 into slots 0 and 1.
+    // Barrier after LDS stores that other waves read (tables, the next work code): lgkmcnt(0) first.
+    auto lds_barrier = [&]() {
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    // The whole set-up of one item without prefetch: offsets, tables into buffer tb, stages 0 and 1
+    // (XPF) into LDS buffers and weight slots 0 and 1. Every wave has passed the previous item's last
+    // barrier, so no wave still reads those buffers.
     auto start_item = [&](const WorkItem& w, int tb) {
         int pr[kPkMB / 2];
 #pragma unroll
@@ -419,14 +451,17 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
             a_cur[i] = a_off(w, kGather ? pr[i] / prm.topk : pr[i]);
         if constexpr (MODE == kModePkDown) rw = prm.route_w[pair];
 #pragma unroll
-        for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_cur, a_cur[i], 0);
+        for (int i = 0; i < kPkMB / 2; ++i) copy_a(ra_cur, a_cur[i], 0, IC<0>{}, i);
 #pragma unroll
         for (int q = 0; q < 4; ++q) breg[0][q] = b_ld(rb_cur, bstep_cur, 0, q);
+        if constexpr (XPF) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) breg[1][q] = b_ld(rb_cur, bstep_cur, min(1, nst - 1), q);
+            for (int i = 0; i < kPkMB / 2; ++i) copy_a(ra_cur, a_cur[i], 1, IC<1>{}, i);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) breg[1][q] = b_ld(rb_cur, bstep_cur, 1, q);
+        }
         tab_store(tb, pair, rw, bias, wx);
-        __syncthreads();  // without prefetch the previous item's only step may still read buffer 0
-        store_a(IC<kPkMB / 2>{}, IC<0>{});
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tables are read after the first step's barrier
     };
     start_item(cur, 0);
     if (n_tail > 0 && wave == 0) {  // the tail table (read from the first item's end on; k-loop barriers order it)
@@ -446,8 +481,8 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         if (lane == 0) s_ntail = n_tail + __popcll(sb);
     }
 
-    int par = 0;  // LDS buffer / weight slot of the current item's stage 0
-    for (int j = 0;; ++j) {
+    // One item; false once the work is done.
+    auto item = [&](int j) -> bool {
         WorkItem nx;
         const bool has_nx = item_at(it_nx, nx);
         if (!has_nx) nx = cur;  // past the end the "next" loads re-read the current item
@@ -458,76 +493,85 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         const bool active = wave < prm.fw && fc < prm.NF;  // wave-uniform
         const int nmb = ceil_div(rows, 32);  // non-empty 32-row blocks
         const int tb = j & 1;                // table buffer of this item
+        // The next item's rows (GEMM1: their pair ids, loaded here, an item ahead of the copies that use them).
+        int nxr[kPkMB / 2];
+        if constexpr (XPF) {
+#pragma unroll
+            for (int i = 0; i < kPkMB / 2; ++i) {
+                if constexpr (kGather) nxr[i] = prm.sorted_pairs[a_row(nx, i)];
+                else nxr[i] = a_row(nx, i);
+            }
+        }
 #pragma unroll
         for (int mb = 0; mb < kPkMB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
 
-        // The k-loop. Step s runs the MFMAs of stage s from LDS buffer and weight slot (par + s) & 1,
-        // loads the activation chunks of stage s+1 at its start (written to the other buffer at its
-        // end) and, k-step by k-step, the weights of stage s+2 into the slot just consumed. In the
-        // last two steps "stage s+1 / s+2" are stages 0 and 1 of the next item (XPF), whose row
-        // offsets and tables are loaded there too, so the weights keep streaming through the
-        // epilogue. Loads and MFMAs are never behind a branch: the compiler's waits stay exact and
-        // each step is one basic block.
-        auto kloop = [&](auto nc, auto pc) {
+        // The k-loop runs over positions p = 0 .. NP-1, NP = nst rounded up to a multiple of 3: positions
+        // below nst are the stages, the one or two above (if any) are empty. Position p uses LDS buffer and
+        // weight register slot p % 3, so every item starts in buffer and slot 0 and its last two positions
+        // are always in buffers 1 and 2. Step p runs the MFMAs of stage p, copies the activation rows of
+        // stage p+2 into the buffer freed by step p-1 at its start and, k-step by k-step, loads the weights
+        // of stage p+2 into the slot freed by step p-1: both operands arrive two steps ahead, and a step's
+        // wait covers only its own stage. The last two positions load stages 0 and 1 of the next item
+        // (XPF) instead, with its row offsets and tables, so the weights and activations keep streaming
+        // through the epilogue (where the positions are empty, they have no MFMAs and the next item's
+        // stages land during the epilogue). Loads and MFMAs are never behind a branch: the compiler's waits
+        // stay exact and each step is one basic block.
+        auto kloop = [&](auto nc) {
             constexpr int NMB = decltype(nc)::value;  // 32-row blocks computed; 0: idle wave
-            constexpr int PP = decltype(pc)::value;   // parity of stage 0
-            // Activation chunks per thread per stage. The tile is shared: an idle wave still loads
+            // Activation chunks per thread per stage. The tile is shared: an idle wave still copies
             // its rows (all four chunks; rows past the item's blocks are never read).
             constexpr int NA = NMB > 0 ? (NMB + 1) / 2 : kPkMB / 2;
-            int nxr[kPkMB / 2];                       // next item's rows (GEMM1: pair ids), KIND 1 -> 2
             int npair = 0, nwx = 0;
             float nbias = 0.f;
-            // KIND 0: ordinary step; 1: second to last (next item's weight stage 0, rows, tables);
-            // 2: last (next item's activation stage 0, all 256 rows, and weight stage 1).
-            auto step = [&](int s, auto bc, auto kc) {
+            // KIND 0: a stage, with the copies and weight loads of stage p + 2; 3: a stage whose p + 2 is
+            // an empty position (no loads); 1: position NP-2 (next item's rows, stage 0, tables);
+            // 2: position NP-1 (next item's stage 1, routing weights; all 256 rows of both stages).
+            // EMPTY: a position past the last stage (no MFMAs).
+            auto step = [&](int s, auto bc, auto kc, auto ec) {
                 constexpr int b = decltype(bc)::value;
+                constexpr int bn = (b + 2) % 3;  // buffer and slot of position p + 2
                 constexpr int KIND = decltype(kc)::value;
-                __syncthreads();  // stage s is in LDS buffer b; every wave is done with the other buffer
-                const unsigned char* sA = smem + b * kPkABytes;
+                constexpr bool EMPTY = decltype(ec)::value;
+                constexpr bool kNext = (KIND == 1 || KIND == 2) && XPF;  // loads for the next item
+                constexpr bool kLoadW = KIND == 0 || kNext;
+                const uint32_t probe = stage_barrier(IC<b>{});  // stage p is in LDS buffer b; buffer bn is free
+                const unsigned char* sA = sbuf(IC<b>{});
                 auto read_af = [&](int q, int mb) {
                     return *reinterpret_cast<const OpT*>(sA + lds_off(mb * 32 + (lane & 31), 2 * q + (lane >> 5)));
                 };
                 float nw = 0.f;
-                if constexpr (KIND == 2) {
-                    if constexpr (XPF) {
+                if constexpr (KIND == 0) {
+#pragma unroll
+                    for (int i = 0; i < NA; ++i) copy_a(ra_cur, a_cur[i], s + 2, IC<bn>{}, i);
+                } else if constexpr (kNext) {
+                    if constexpr (KIND == 1) {
 #pragma unroll
                         for (int i = 0; i < kPkMB / 2; ++i)
                             a_cur[i] = a_off(nx, kGather ? nxr[i] / prm.topk : nxr[i]);
-#pragma unroll
-                        for (int i = 0; i < kPkMB / 2; ++i) areg[i] = a_ld(ra_nx, a_cur[i], 0);
-                        if constexpr (MODE == kModePkDown) {
-                            nw = prm.route_w[npair];
-                            nwx = tab_wexp(nx);
-                        }
-                    }
-                } else {
-#pragma unroll
-                    for (int i = 0; i < NA; ++i) areg[i] = a_ld(ra_cur, a_cur[i], s + 1);
-                    if constexpr (KIND == 1) {
-#pragma unroll
-                        for (int i = 0; i < kPkMB / 2; ++i) {
-                            if constexpr (kGather) nxr[i] = prm.sorted_pairs[a_row(nx, i)];
-                            else nxr[i] = a_row(nx, i);
-                        }
                         if constexpr (MODE == kModePkDown) npair = tab_pair(nx);
                         if constexpr (HAS_BIAS) nbias = tab_bias(nx);
+                    } else if constexpr (MODE == kModePkDown) {
+                        nw = prm.route_w[npair];
+                        nwx = tab_wexp(nx);
                     }
+#pragma unroll
+                    for (int i = 0; i < kPkMB / 2; ++i) copy_a(ra_nx, a_cur[i], KIND - 1, IC<bn>{}, i);
                 }
                 // A fragments in a ring of R registers: MFMA k (k-step k / NMB, block k % NMB) reads
                 // slot k % R, which is then refilled with fragment k + R, R MFMAs ahead of its use.
                 constexpr int R = NMB < 4 ? (NMB > 0 ? NMB : 1) : 4;
                 constexpr int NK = 4 * NMB;
                 OpT af[R];
-                if constexpr (NMB > 0) {
+                if constexpr (NMB > 0 && !EMPTY) {
 #pragma unroll
                 for (int k = 0; k < R; ++k) af[k] = read_af(k / NMB, k % NMB);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     // Raised wave priority for the k-step's MFMA group: while the other wave of the SIMD is
-                    // in its step's non-MFMA part (first LDS reads, LDS writes, barrier), the wave that has
-                    // MFMAs to issue wins the arbitration, which keeps the shared matrix unit fed.
+                    // in its step's non-MFMA part (first LDS reads, barrier), the wave that has MFMAs to
+                    // issue wins the arbitration, which keeps the shared matrix unit fed.
                     __builtin_amdgcn_sched_barrier(0);
                     __builtin_amdgcn_s_setprio(1);
                     __builtin_amdgcn_sched_barrier(0);
@@ -543,8 +587,8 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                             acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bq, af[k % R], acc[mb], 0, 0, 0);
                         if (k + R < NK) af[k % R] = read_af((k + R) / NMB, (k + R) % NMB);
                     }
-                    if constexpr (KIND == 0) breg[b][q] = b_ld(rb_cur, bstep_cur, s + 2, q);
-                    else if constexpr (XPF) breg[b][q] = b_ld(rb_nx, bstep_nx, KIND - 1, q);
+                    if constexpr (KIND == 0) breg[bn][q] = b_ld(rb_cur, bstep_cur, s + 2, q);
+                    else if constexpr (kNext) breg[bn][q] = b_ld(rb_nx, bstep_nx, KIND - 1, q);
                     // Keep the order written above: MFMA, then the LDS read that refills its A
                     // register, block by block; then the weight load.
 #pragma unroll
@@ -552,65 +596,59 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                            // MFMA
                         if (q * NMB + mb + R < NK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
                     }
-                    if (KIND == 0 || XPF) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+                    if (kLoadW) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
                     __builtin_amdgcn_sched_barrier(0);
                     __builtin_amdgcn_s_setprio(0);
                 }
-                } else if constexpr (KIND != 0 && XPF) {
-                    // An idle wave may be active in the next item: its first two weight stages are
-                    // prefetched all the same.
+                } else if constexpr (kNext) {
+                    // An idle wave may be active in the next item (and an empty position has no MFMAs): the
+                    // next item's first two weight stages are loaded all the same.
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) breg[b][q] = b_ld(rb_nx, bstep_nx, KIND - 1, q);
+                    for (int q = 0; q < 4; ++q) breg[bn][q] = b_ld(rb_nx, bstep_nx, KIND - 1, q);
                 }
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (KIND == 2) {
-                    if constexpr (XPF) {
-                        store_a(IC<kPkMB / 2>{}, IC<1 - b>{});
-                        tab_store(tb ^ 1, npair, nw, nbias, nwx);
-                    }
-                } else {
-                    store_a(IC<NA>{}, IC<1 - b>{});
-                }
+                if constexpr (KIND == 2 && XPF) tab_store(tb ^ 1, npair, nw, nbias, nwx);
+                asm volatile("" ::"v"(probe));
             };
-            const int M = nst - 2;  // ordinary steps
-            int s = 0;
-            for (; s + 1 < M; s += 2) {
-                step(s, IC<PP>{}, IC<0>{});
-                step(s + 1, IC<1 - PP>{}, IC<0>{});
-            }
-            if constexpr (ODD) {
-                if constexpr (XPF) {
-                    step(s, IC<PP>{}, IC<0>{});  // M is odd
-                    step(nst - 2, IC<1 - PP>{}, IC<1>{});
+            if constexpr (XPF) {
+                // positions 0 .. nst-3 load stage p + 2: rounds of three, then L = (nst - 2) % 3 left over;
+                // then E = NP - nst stages whose p + 2 is empty, then positions NP-2 and NP-1 (buffers 1, 2)
+                constexpr int L = (R3 + 1) % 3, E = (3 - R3) % 3;
+                const int M = nst - 2;
+                int s = 0;
+                for (; s + 3 <= M; s += 3) {
+                    step(s, IC<0>{}, IC<0>{}, IC<false>{});
+                    step(s + 1, IC<1>{}, IC<0>{}, IC<false>{});
+                    step(s + 2, IC<2>{}, IC<0>{}, IC<false>{});
                 }
-                step(nst - 1, IC<PP>{}, IC<2>{});
+                if constexpr (L >= 1) step(s, IC<0>{}, IC<0>{}, IC<false>{});
+                if constexpr (L >= 2) step(s + 1, IC<1>{}, IC<0>{}, IC<false>{});
+                if constexpr (E >= 1) step(nst - 2, IC<L % 3>{}, IC<3>{}, IC<false>{});
+                if constexpr (E >= 2) step(nst - 1, IC<(L + 1) % 3>{}, IC<3>{}, IC<false>{});
+                static_assert((L + E) % 3 == 1, "position NP-2 is in buffer 1");
+                step(nst - 2 + E, IC<1>{}, IC<1>{}, IC<(E >= 2)>{});
+                step(nst - 1 + E, IC<2>{}, IC<2>{}, IC<(E >= 1)>{});
             } else {
-                step(nst - 2, IC<PP>{}, IC<1>{});
-                step(nst - 1, IC<1 - PP>{}, IC<2>{});
+                step(0, IC<0>{}, IC<2>{}, IC<false>{});
             }
         };
-        auto dispatch = [&](auto pc) {
+        auto dispatch = [&]() {
             if (!active) {
-                kloop(IC<0>{}, pc);
+                kloop(IC<0>{});
                 return;
             }
             switch (nmb) {
-                case 1: kloop(IC<1>{}, pc); break;
-                case 2: kloop(IC<2>{}, pc); break;
-                case 3: kloop(IC<3>{}, pc); break;
-                case 4: kloop(IC<4>{}, pc); break;
-                case 5: kloop(IC<5>{}, pc); break;
-                case 6: kloop(IC<6>{}, pc); break;
-                case 7: kloop(IC<7>{}, pc); break;
-                default: kloop(IC<8>{}, pc); break;
+                case 1: kloop(IC<1>{}); break;
+                case 2: kloop(IC<2>{}); break;
+                case 3: kloop(IC<3>{}); break;
+                case 4: kloop(IC<4>{}); break;
+                case 5: kloop(IC<5>{}); break;
+                case 6: kloop(IC<6>{}); break;
+                case 7: kloop(IC<7>{}); break;
+                default: kloop(IC<8>{}); break;
             }
         };
-        if constexpr (XPF && ODD) {
-            if (par) dispatch(IC<1>{});
-            else dispatch(IC<0>{});
-        } else {
-            dispatch(IC<0>{});
-        }
+        dispatch();
         if (tid == 0) s_next = item_of_off(2 * slots + ticket);
 
         // ---- epilogue: element r of a transposed 32x32 accumulator block is row lane & 31 of the
@@ -761,21 +799,26 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 }
             }
         }
-        __syncthreads();  // s_next
-        const int it_nn = s_next;
-        if (!has_nx) break;  // tickets are drawn in increasing order: the held one is past the end too
+        lds_barrier();  // s_next
+        // The same value in every lane; readfirstlane tells the compiler so, which keeps the item decode and
+        // the operand descriptors in scalar registers (otherwise every weight load gets a waterfall loop).
+        const int it_nn = __builtin_amdgcn_readfirstlane(s_next);
+        if (!has_nx) {  // tickets are drawn in increasing order: the held one is past the end too
+            // the prefetch copies into LDS land before the workgroup (and its LDS) is gone
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            return false;
+        }
         it_nx = it_nn;
         if (tid == 0) ticket = atomicAdd(prm.counters + xcd, 1);
         cur = nx;
         ra_cur = ra_nx;
         rb_cur = rb_nx;
         bstep_cur = bstep_nx;
-        if constexpr (XPF) {
-            if constexpr (ODD) par ^= 1;
-        } else {
-            start_item(cur, tb ^ 1);
-        }
-    }
+        if constexpr (!XPF) start_item(cur, tb ^ 1);
+        return true;
+    };
+    for (int j = 0;; ++j)
+        if (!item(j)) break;
 }
 
 static int g_pk_cu_count = 0;
@@ -802,12 +845,14 @@ template <int MODE, int ACT, bool HAS_BIAS>
 static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s) {
     const int grid = pk_grid(max_tiles, prm.n_tiles);
     const int nst = prm.Kd / kBK;
-    if (nst >= 2 && (nst & 1) == 0)
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
-    else if (nst >= 2)
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, true>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    if (nst < 2)
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, false, 1>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    else if (nst % 3 == 0)
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 0>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    else if (nst % 3 == 1)
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 1>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     else
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, false, true>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 2>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     return hipGetLastError();
 }
 
