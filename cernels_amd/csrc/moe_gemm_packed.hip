@@ -245,10 +245,12 @@ using IC = std::integral_constant<int, N>;
 
 // MODE/ACT/HAS_BIAS select the projection; XPF: the reduction has at least two stages, and the
 // next item's first two stages are copied and loaded during the current item's last two steps
-// (cross-item prefetch); R3: the number of stages mod 3, which sets the k-loop's empty positions.
-template <int MODE, int ACT, bool HAS_BIAS, bool XPF, int R3>
+// (cross-item prefetch); R3: the number of stages mod 3, which sets the k-loop's empty positions;
+// PEEL (R3 == 2, at least 5 stages): the loop's last round of three steps runs after it.
+template <int MODE, int ACT, bool HAS_BIAS, bool XPF, int R3, bool PEEL>
 __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams prm) {
     static_assert(XPF || R3 == 1, "without prefetch the reduction is one stage");
+    static_assert(!PEEL || R3 == 2, "peeled only where no ordinary step follows the loop");
     static_assert(MODE != kModePkUp || !HAS_BIAS, "the non-gated projection has no bias");
     static_assert(MODE != kModePkDown || !HAS_BIAS, "the down bias is added by the combine");
     // GEMM2 multiplies fp16 glu by fp16 weights; the first projections bf16 x by bf16 weights.
@@ -367,14 +369,21 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     auto tab_wexp = [&](const WorkItem& w) {
         return (int)prm.wexp[(long long)w.e * prm.NF + min(w.n_idx * prm.fw + (tid & (kPkWaves - 1)), prm.NF - 1)];
     };
+    // The row index is rebuilt here from the wave index (scalar) and the lane index (v_mbcnt, no inputs;
+    // in asm, so that the compiler does not fold it back into the lane register it keeps): this store runs
+    // at the end of the k-loop, where reloading a spilled lane register would wait for every load in flight.
     auto tab_store = [&](int buf, int pair, float w, float bias, int wx) {
-        if (tid < kPkBM) {
+        static_assert(kPkBM % kWave == 0, "the table rows are whole waves");
+        if (wave < kPkBM / kWave) {
+            int l;
+            asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+            const int t = wave * kWave + l;
             if constexpr (MODE == kModePkDown) {
-                s_pair[buf][tid] = pair;
-                s_w[buf][tid] = w;
-                s_wx[buf][tid] = wx;
+                s_pair[buf][t] = pair;
+                s_w[buf][t] = w;
+                s_wx[buf][t] = wx;
             }
-            if constexpr (HAS_BIAS) s_bias[buf][tid] = bias;
+            if constexpr (HAS_BIAS) s_bias[buf][t] = bias;
         }
     };
 
@@ -561,7 +570,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 }
                 // A fragments in a ring of R registers: MFMA k (k-step k / NMB, block k % NMB) reads
                 // slot k % R, which is then refilled with fragment k + R, R MFMAs ahead of its use.
-                constexpr int R = NMB < 4 ? (NMB > 0 ? NMB : 1) : 4;
+                constexpr int R = NMB < 3 ? (NMB > 0 ? NMB : 1) : 3;
                 constexpr int NK = 4 * NMB;
                 OpT af[R];
                 if constexpr (NMB > 0 && !EMPTY) {
@@ -616,10 +625,19 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 constexpr int L = (R3 + 1) % 3, E = (3 - R3) % 3;
                 const int M = nst - 2;
                 int s = 0;
-                for (; s + 3 <= M; s += 3) {
+                // With no ordinary step between the loop and the last positions (L = 0), the compiler
+                // reassigns the weight registers at the loop's exit and waits there for every load in flight;
+                // running the loop's last round after it (PEEL) avoids that.
+                for (; s + 3 + (PEEL ? 3 : 0) <= M; s += 3) {
                     step(s, IC<0>{}, IC<0>{}, IC<false>{});
                     step(s + 1, IC<1>{}, IC<0>{}, IC<false>{});
                     step(s + 2, IC<2>{}, IC<0>{}, IC<false>{});
+                }
+                if constexpr (PEEL) {
+                    step(s, IC<0>{}, IC<0>{}, IC<false>{});
+                    step(s + 1, IC<1>{}, IC<0>{}, IC<false>{});
+                    step(s + 2, IC<2>{}, IC<0>{}, IC<false>{});
+                    s += 3;
                 }
                 if constexpr (L >= 1) step(s, IC<0>{}, IC<0>{}, IC<false>{});
                 if constexpr (L >= 2) step(s + 1, IC<1>{}, IC<0>{}, IC<false>{});
@@ -846,13 +864,15 @@ static hipError_t launch_pk_t(const PkParams& prm, int max_tiles, hipStream_t s)
     const int grid = pk_grid(max_tiles, prm.n_tiles);
     const int nst = prm.Kd / kBK;
     if (nst < 2)
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, false, 1>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, false, 1, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     else if (nst % 3 == 0)
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 0>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 0, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     else if (nst % 3 == 1)
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 1>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 1, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+    else if (nst >= 5)
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 2, true>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     else
-        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 2>), dim3(grid), dim3(kPkThreads), 0, s, prm);
+        hipLaunchKernelGGL((moe_gemm_packed_kernel<MODE, ACT, HAS_BIAS, true, 2, false>), dim3(grid), dim3(kPkThreads), 0, s, prm);
     return hipGetLastError();
 }
 
