@@ -151,8 +151,9 @@ __global__ __launch_bounds__(kV3Threads, 1) void moe_gemm_v3_kernel(GemmParams p
         const int local = it - t0 * prm.n_tiles;
         const int n_idx = local / nt_e, m_idx = local - n_idx * nt_e;
         const int seg0 = prm.offsets[e], seg_n = prm.offsets[e + 1] - seg0;
-        const int row_begin = seg0 + m_idx * kV3BM;
-        const int rows = min(kV3BM, seg_n - m_idx * kV3BM);
+        int row_begin, rows;  // the expert's M-tiles split its rows evenly in 32-row blocks
+        tile_rows(m_idx, nt_e, seg_n, row_begin, rows);
+        row_begin += seg0;
         const int n0 = n_idx * (MODE == kModeGateUp ? halfN : kV3BN);  // first output column
         const uint16_t* Be = prm.B + (long long)e * prm.expert_stride;
         const int Kd = prm.Kdim;

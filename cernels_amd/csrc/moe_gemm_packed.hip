@@ -313,7 +313,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     __shared__ int s_ntail;
     auto item_at = [&](int code, WorkItem& w) {  // code: work code, or -1
         if (code < 0) return false;
-        w = decode_item(code >> 2, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
+        w = decode_item(code >> 2, prm.n_tiles, prm.tile_expert, prm.tile_offsets, prm.offsets);
         tail_part(code & 3, kPkBM, w.row_begin, w.rows);
         return true;
     };
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         const int it = b_lo + n_whole + lane;
         bool split = false;
         if (lane < n_tail) {
-            const WorkItem w = decode_item(it, prm.n_tiles, kPkBM, prm.tile_expert, prm.tile_offsets, prm.offsets);
+            const WorkItem w = decode_item(it, prm.n_tiles, prm.tile_expert, prm.tile_offsets, prm.offsets);
             split = tail_splits(w.rows, kPkBM);
         }
         const uint64_t sb = __ballot(split);

@@ -68,6 +68,19 @@ CMOE_HD inline void split_clamp(int* b, int total, int slots) {
     b[8] = total;
 }
 
+// Rows of M-tile m of an expert with `rows` rows in nt = ceil(rows / bm) M-tiles (bm a multiple of 32): the
+// tiles split the rows evenly in 32-row blocks, tile m taking blocks [m nb / nt, (m+1) nb / nt) of the
+// nb = ceil(rows / 32), rather than bm, bm, ..., remainder. The tiles that share an N-tile's weights then run
+// their k-loops at the same speed and stay together in the XCD's L2 (a remainder tile of a few rows ran ahead of
+// its full siblings and fetched the weights again). Every tile has 1 .. bm/32 blocks (nb <= (bm / 32) nt), the
+// same number of 32-row MFMA blocks in total.
+CMOE_HD inline void tile_rows(int m, int nt, int rows, int& row_begin, int& tile_rows_out) {
+    const long long nb = (rows + 31) / 32;
+    const int b0 = (int)(m * nb / nt), b1 = (int)((m + 1) * nb / nt);
+    row_begin = 32 * b0;
+    tile_rows_out = (32 * b1 < rows ? 32 * b1 : rows) - 32 * b0;
+}
+
 // The tail of one XCD's item range (the packed gate_up GEMM): where the range holds at least three rounds of items
 // for its slots, its last min(tail, max_tail, n_items - 2 slots) items are handed out as two halves when they
 // have more than 3/4 bm rows. The first two offsets of every slot (taken before the tail table exists) are

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "moe_common.h"
+#include "moe_split.h"
 
 namespace cmoe {
 
@@ -37,12 +38,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void wait_all_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Grouped-GEMM work item: items are (expert, N-tile, M-tile) in expert-major order with M fastest,
-// numbered over the M-tile list the route kernel wrote (tile_expert, tile_offsets, offsets).
+// numbered over the M-tile list the route kernel wrote (tile_expert, tile_offsets, offsets); an expert's
+// M-tiles split its rows as tile_rows does.
 struct WorkItem {
     int e, n_idx, row_begin, rows;
 };
 
-__device__ __forceinline__ WorkItem decode_item(int it, int n_tiles, int bm, const int32_t* __restrict__ tile_expert,
+__device__ __forceinline__ WorkItem decode_item(int it, int n_tiles, const int32_t* __restrict__ tile_expert,
                                                 const int32_t* __restrict__ tile_offsets,
                                                 const int32_t* __restrict__ offsets) {
     WorkItem w;
@@ -51,9 +53,9 @@ __device__ __forceinline__ WorkItem decode_item(int it, int n_tiles, int bm, con
     const int local = it - t0 * n_tiles;
     w.n_idx = local / nt_e;
     const int m_idx = local - w.n_idx * nt_e;
-    const int seg0 = offsets[w.e], seg_n = offsets[w.e + 1] - seg0;
-    w.row_begin = seg0 + m_idx * bm;
-    w.rows = min(bm, seg_n - m_idx * bm);
+    const int seg0 = offsets[w.e];
+    tile_rows(m_idx, nt_e, offsets[w.e + 1] - seg0, w.row_begin, w.rows);
+    w.row_begin += seg0;
     return w;
 }
 

@@ -190,3 +190,33 @@ def test_tail_halves_cover_every_row_once(split_exe):
         assert [i for i, _, _, _ in codes] == sorted(i for i, _, _, _ in codes)
         halved += sum(h == 2 for _, h, _, _ in codes)
     assert halved > 0
+
+
+def test_tile_rows_split_each_expert_evenly(split_exe):
+    """An expert's M-tiles (moe_split.h tile_rows, used by both grouped GEMMs' item decode): ceil(rows / bm)
+    tiles that cover the rows in order, exactly once, each starting on a 32-row block and holding 1 .. bm/32
+    blocks, block counts that differ by at most one between tiles, and ceil(rows / 32) blocks in total (as many
+    32-row MFMA blocks as bm, bm, ..., remainder tiles have)."""
+    rng = np.random.default_rng(11)
+    cases = [(r, bm) for bm in (128, 256) for r in range(1, 1100)]
+    cases += [(int(r), bm) for bm in (128, 256) for r in rng.integers(1, 1 << 22, size=200)]
+    cases += [(bm * bm + d, bm) for bm in (128, 256) for d in (-1, 0, 1)] + [((1 << 24) - 1, 256), (1 << 24, 128)]
+    text = "".join(f"R {r} {bm}\n" for r, bm in cases)
+    out = subprocess.run([str(split_exe)], input=text, capture_output=True, text=True, check=True).stdout
+    tiles, cur = [], []
+    for line in out.strip().splitlines():
+        if line == "END":
+            tiles.append(cur)
+            cur = []
+        else:
+            cur.append(tuple(map(int, line.split())))
+    assert len(tiles) == len(cases)
+    for (rows, bm), ts in zip(cases, tiles):
+        assert len(ts) == -(-rows // bm), (rows, bm)
+        nxt = 0
+        for rb, r in ts:
+            assert rb == nxt and rb % 32 == 0 and 1 <= r <= bm, (rows, bm, rb, r)
+            nxt = rb + r
+        assert nxt == rows
+        blocks = [-(-r // 32) for _, r in ts]
+        assert sum(blocks) == -(-rows // 32) and max(blocks) - min(blocks) <= 1, (rows, bm, blocks)

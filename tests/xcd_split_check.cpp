@@ -6,7 +6,9 @@
 //   "D a b" -> split_floordiv(a, b);
 //   "T n slots tail bm rows_0 .. rows_{n-1}" (the items of one XCD range) -> one line per work offset,
 //     "item h row_begin rows" (row_begin relative to the item), in the order the packed gate_up GEMM hands
-//     them out: the whole items before the tail, then the tail table (items in order, halves in order).
+//     them out: the whole items before the tail, then the tail table (items in order, halves in order);
+//   "R rows bm" -> the M-tiles of an expert with `rows` rows (ceil(rows / bm) of them, tile_rows), one line
+//     "row_begin rows" each, then "END".
 #include <cstdio>
 #include <vector>
 
@@ -19,6 +21,18 @@ int main() {
             long long a, b;
             if (std::scanf("%lld %lld", &a, &b) != 2) return 1;
             std::printf("%d\n", cmoe::split_floordiv(a, b));
+            continue;
+        }
+        if (op == 'R') {
+            int rows, bm;
+            if (std::scanf("%d %d", &rows, &bm) != 2) return 1;
+            const int nt = (rows + bm - 1) / bm;
+            for (int m = 0; m < nt; ++m) {
+                int rb = 0, r = 0;
+                cmoe::tile_rows(m, nt, rows, rb, r);
+                std::printf("%d %d\n", rb, r);
+            }
+            std::printf("END\n");
             continue;
         }
         if (op == 'T') {
