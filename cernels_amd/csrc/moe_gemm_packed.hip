@@ -327,9 +327,9 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     // Operands are read with buffer loads: a 128-bit descriptor per operand and item (uniform,
     // SGPRs) plus a 32-bit per-lane offset, so the k-loop holds no 64-bit addresses.
     //   A: GEMM1 gathers token rows of x (descriptor over all of x); GEMM2 reads the item's own
-    //      contiguous glu rows (descriptor at its first row). Thread t reads rows t/8 + 64i of the
-    //      tile, clamped to the item's last row: a_row() is the row in the A matrix, a_off() its byte
-    //      offset from the descriptor base.
+    //      contiguous glu rows (descriptor at its first row). Thread t copies rows t/8 + 64i of the
+    //      tile into LDS, clamped to the item's last row: a_row() is the row in the A matrix, a_off()
+    //      its byte offset from the descriptor base (at the chunk this lane copies).
     //   B: the wave's fragment run from k-step 0; lane offset lane*16, k-step offsets uniform.
     auto a_row = [&](const WorkItem& w, int i) { return w.row_begin + min((tid >> 3) + 64 * i, w.rows - 1); };
     auto a_off = [&](const WorkItem& w, int src_row) {
