@@ -55,11 +55,12 @@ constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 
 constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
 constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
 constexpr int kPkMaxTail = 16;              // most items split into halves at the end of an XCD's range
-// Items split at the end of each XCD's range: 12 for gate_up, none for down. Measured in one process against
-// no split (two alternations, µs per launch): gate_up 572.7/565.6 -> 559.4/557.3 on gpt-oss and 245.6/247.8 ->
-// 240.6/240.6 on the Zipf workload (16 and 24 items: within a few µs of 12); down 332.7/327.1 -> 339.3/339.9 on
-// gpt-oss, where a half item costs more of its full item's time (its activation tile and its weights are the
-// same) than the shorter tail gains.
+// Items split at the end of each XCD's range: 12 for gate_up where experts average fewer rows than one M-tile,
+// none otherwise and none for down. A half item keeps its full item's weight stream for half the MFMA work, so
+// the split pays only where item costs are uneven. Measured in one process against no split (two alternations,
+// gate_up µs per launch): Zipf (80 rows per expert) 241.3/245.5 -> 235.3/233.3; gpt-oss (512 rows per expert, whose
+// M-tiles split its rows evenly) 502.8/502.6 -> 512.5/510.1 (16 items: within a few µs of 12); down with 8 or
+// 12 items: equal or up to 12 µs slower on gpt-oss.
 constexpr int kPkTailGateUp = 12;
 // glu segments: scaled up below this largest |glu| (2^-8), down at or above 2^15; an all-zero segment
 // records kGluAnyScale in gexp
@@ -1056,7 +1057,7 @@ hipError_t launch_prefill_packed(const void* x, const void* w1p, const float* b1
     g1.rsig = rsig;
     g1.sync = meta + 24;
     g1.p_cap = T * K;
-    g1.tail = kPkTailGateUp;
+    g1.tail = (long long)T * K < (long long)kPkBM * E ? kPkTailGateUp : 0;  // fewer rows per expert than one M-tile
     if (act == kActSilu)
         st = b1 ? launch_pk_t<kModePkGateUp, kActSilu, true>(g1, max_tiles, s)
                 : launch_pk_t<kModePkGateUp, kActSilu, false>(g1, max_tiles, s);
