@@ -53,7 +53,7 @@ constexpr int kPkMB = kPkBM / 32;           // 32-row MFMA blocks per item
 constexpr int kPkABytes = kPkBM * kBK * 2;  // 32 KB A stage
 constexpr int kPkFrag = 512;                // bf16 elements of one fragment (1 KB)
 constexpr int kPkGlu = kPkWaves * 16;       // glu columns of a GEMM1 N-tile
-constexpr int kPkBDepth = 2;                // weight stages held in registers per wave
+constexpr int kPkStages = 3;                // activation LDS buffers = weight register slots per wave
 constexpr int kPkMaxTail = 16;              // most items split into halves at the end of an XCD's range
 // Items split at the end of each XCD's range: 12 for gate_up where experts average fewer rows than one M-tile,
 // none otherwise and none for down. A half item keeps its full item's weight stream for half the MFMA work, so
@@ -401,7 +401,8 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
     const uint32_t b_lane = (uint32_t)lane * 16u;
 
     f32x16 acc[kPkMB];
-    u32x4 breg[3][4];  // weight fragments: slot d holds the four k-steps of one stage
+    static_assert(kPkStages == 3, "three LDS arrays below and the mod-3 step schedule of the k-loop");
+    u32x4 breg[kPkStages][4];  // weight fragments: slot d holds the four k-steps of one stage
     auto sbuf = [&](auto bc) -> unsigned char* {
         constexpr int b = decltype(bc)::value;
         if constexpr (b == 0) return sA0;
