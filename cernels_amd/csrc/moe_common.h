@@ -52,13 +52,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 // never reach the output.
 //   silu:   transformers ACT2FN["silu"] = x * sigmoid(x)  (modeling_cohere2_moe.py:131)
 //   gpt-oss: GptOssExperts._apply_gate (modeling_gpt_oss.py:82-88), alpha 1.702, limit 7.0
+// The clamps are IEEE minimum/maximum (v_minimum3_f32 / v_maximum3_f32): a nan propagates, as through
+// torch.clamp in the transformers module (fminf / fmaxf, as in src/kops/gpt_oss_moe_experts/csrc/
+// gpt_oss_moe_experts.cu:98-99, would clamp it to a finite +-7).
 template <int ACT>
 __device__ __forceinline__ float swiglu(float gate, float up) {
     if constexpr (ACT == kActSilu) {
         return gate * __builtin_amdgcn_rcpf(1.0f + __expf(-gate)) * up;
     } else {
-        gate = fminf(gate, 7.0f);
-        up = fminf(fmaxf(up, -7.0f), 7.0f);
+        gate = __builtin_elementwise_minimum(gate, 7.0f);
+        up = __builtin_elementwise_minimum(__builtin_elementwise_maximum(up, -7.0f), 7.0f);
         const float glu = gate * __builtin_amdgcn_rcpf(1.0f + __expf(-1.702f * gate));
         return (up + 1.0f) * glu;
     }
@@ -76,7 +79,7 @@ __device__ __forceinline__ float act_plain(float h) {
     } else if constexpr (ACT == kActSiluPlain) {
         return h * __builtin_amdgcn_rcpf(1.0f + __expf(-h));
     } else {
-        return fmaxf(h, 0.0f);
+        return __builtin_elementwise_maximum(h, 0.0f);  // a nan propagates, as through torch.relu
     }
 }
 
@@ -93,20 +96,24 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 // 24-bit floats: the top 24 bits of the fp32 pattern (sign, 8-bit exponent, 15-bit mantissa), rounded
 // to nearest even on the 8 dropped bits (2^-16 relative rounding, fp32's range; values past the largest
 // 24-bit float round to inf). inf stays inf; a nan becomes the quiet nan (its rounding could carry it
-// into inf). Branch-free: five VALU instructions per value. Four of them pack into three dwords, value
-// i in bytes 3i..3i+2.
-__device__ __forceinline__ uint32_t f32_to_f24(float f) {
+// into inf). Four values pack into three dwords, value i in bytes 3i..3i+2.
+// f32_round24: the fp32 pattern with the rounding added, whose top 24 bits are the 24-bit float (the low
+// byte is left over); four VALU instructions per value.
+__device__ __forceinline__ uint32_t f32_round24(float f) {
     const uint32_t u = __float_as_uint(f);
-    const uint32_t r = (u + 0x7fu + ((u >> 8) & 1u)) >> 8;
-    return __builtin_isnan(f) ? 0x7fc000u : r;
+    const uint32_t r = u + 0x7fu + ((u >> 8) & 1u);
+    return __builtin_isnan(f) ? 0x7fc00000u : r;
 }
 __device__ __forceinline__ float f24_to_f32(uint32_t r) { return __uint_as_float(r << 8); }
 struct f24x4 {
     uint32_t d[3];
 };
+// The three dwords are bytes 1..3 of the four rounded patterns in order, gathered with one v_perm_b32 each
+// (byte k of the result is byte sel_k of {first operand : second operand}, 0..3 the second, 4..7 the first).
 __device__ __forceinline__ f24x4 pack_f24x4(float a, float b, float c, float e) {
-    const uint32_t r0 = f32_to_f24(a), r1 = f32_to_f24(b), r2 = f32_to_f24(c), r3 = f32_to_f24(e);
-    return f24x4{{r0 | (r1 << 24), (r1 >> 8) | (r2 << 16), (r2 >> 16) | (r3 << 8)}};
+    const uint32_t r0 = f32_round24(a), r1 = f32_round24(b), r2 = f32_round24(c), r3 = f32_round24(e);
+    return f24x4{{__builtin_amdgcn_perm(r1, r0, 0x05030201u), __builtin_amdgcn_perm(r2, r1, 0x06050302u),
+                  __builtin_amdgcn_perm(r3, r2, 0x07060503u)}};
 }
 __device__ __forceinline__ f32x4 unpack_f24x4(const f24x4& p) {
     return f32x4{f24_to_f32(p.d[0] & 0xffffffu), f24_to_f32((p.d[0] >> 24) | ((p.d[1] & 0xffffu) << 8)),

@@ -807,13 +807,16 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     if (row < rows) {
                         const float ws = wsc * s_w[tb][row];  // exact: wsc is a power of two
                         const long long p = s_pair[tb][row];
+                        // this lane's first four columns of the row; the other three groups are 24, 48 and 72
+                        // bytes further (the stores' immediate offsets: one address per row, not per store)
+                        unsigned char* yrow = Yb + (p * prm.H + 32 * fc + c4) * 3;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             float a[4];
 #pragma unroll
                             for (int jj = 0; jj < 4; ++jj) a[jj] = acc[mb][4 * i + jj] * ws;
                             const f24x4 q = pack_f24x4(a[0], a[1], a[2], a[3]);
-                            __builtin_memcpy(Yb + (p * prm.H + 32 * fc + 8 * i + c4) * 3, &q, 12);
+                            __builtin_memcpy(yrow + 24 * i, &q, 12);
                         }
                     }
                 }

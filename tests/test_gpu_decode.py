@@ -104,3 +104,18 @@ def test_decode_baseline_full_size(device, name):
     st = assert_within_tolerance(out, oracle_fp64(c), name, strict=True)
     print(f"[decode full {name}] max|err|/RMS = {st['ratio']:.4f}", flush=True)
     assert_reference_verify(out, oracle_eager(c), name)
+
+
+@pytest.mark.parametrize("layout,act,bias", [("concat", "silu", False), ("concat", "gptoss", True)],
+                         ids=["silu", "gptoss"])
+def test_decode_nan_token_row(device, layout, act, bias):
+    """A token whose hidden state holds a nan gives an all-nan output row (the gpt-oss clamps propagate it, as
+    torch.clamp does); the other tokens' rows are within the bar of the fp64 oracle."""
+    c = rand_case(62, 8, 256, 192, 16, 4, layout=layout, act=act, bias=bias, std=0.05 if bias else 0.02)
+    c["x"][3, 7] = float("nan")
+    print(f"[decode nan row {act}]", flush=True)
+    out = run_gpu(c, device, decode=True).cpu()
+    assert torch.isnan(out[3].float()).all()
+    keep = torch.tensor([0, 1, 2, 4, 5, 6, 7])
+    assert not torch.isnan(out[keep].float()).any()
+    assert_within_tolerance(out[keep], oracle_fp64(c, keep), f"decode nan row {act}")

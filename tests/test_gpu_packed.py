@@ -343,3 +343,20 @@ def test_small_glu_nongated(device):
     rest[tiny] = False
     assert_within_tolerance(out[tiny], ref[tiny], "relu tiny rows", strict=True)
     assert_within_tolerance(out[rest], ref[rest], "relu other rows")
+
+
+@pytest.mark.parametrize("layout,act,bias", [("concat", "silu", False), ("interleaved", "gptoss", True)],
+                         ids=["silu", "gptoss"])
+def test_packed_nan_token_rows(device, layout, act, bias):
+    """A token whose hidden state holds a nan gives an all-nan output row, through the glu segments (a nan
+    is passed over by the segment maximum), the 24-bit Y rows (a nan stays a nan) and the combine; every
+    other token's row is within the bar of the fp64 oracle."""
+    c = rand_case(61, 300, 256, 192, 8, 3, layout=layout, act=act, bias=bias, std=0.05 if bias else 0.02)
+    bad = torch.tensor([0, 17, 299])
+    c["x"][bad, 5] = float("nan")
+    print(f"[packed nan rows {layout}]", flush=True)
+    out = _run_packed(c, device).cpu()
+    assert torch.isnan(out[bad].float()).all()
+    keep = torch.tensor([t for t in range(300) if t not in bad.tolist()])
+    assert not torch.isnan(out[keep].float()).any()
+    assert_within_tolerance(out[keep], oracle_fp64(c, keep), f"nan rows {layout}")

@@ -120,3 +120,20 @@ def test_prefill_baseline_full_size(device, name):
     d3["idx"] = inv[d["idx"].long()].contiguous()
     out_rel = run_gpu(c, device, dev_tensors=d3)
     assert torch.equal(out_rel.view(torch.int16), out.view(torch.int16)), "relabelling the experts changed the output"
+
+
+@pytest.mark.parametrize("layout,act,bias", [("concat", "silu", False), ("interleaved", "gptoss", True)],
+                         ids=["silu", "gptoss"])
+def test_prefill_nan_token_rows(device, layout, act, bias):
+    """The grouped GEMMs on the weights as stored: a token whose hidden state holds a nan gives an all-nan
+    output row (through the bf16 glu pair, the 24-bit Y rows and the combine); the other rows are within the
+    bar of the fp64 oracle."""
+    c = rand_case(63, 300, 256, 192, 8, 3, layout=layout, act=act, bias=bias, std=0.05 if bias else 0.02)
+    bad = torch.tensor([1, 150, 298])
+    c["x"][bad, 9] = float("nan")
+    print(f"[prefill nan rows {layout}]", flush=True)
+    out = run_gpu(c, device).cpu()
+    assert torch.isnan(out[bad].float()).all()
+    keep = torch.tensor([t for t in range(300) if t not in bad.tolist()])
+    assert not torch.isnan(out[keep].float()).any()
+    assert_within_tolerance(out[keep], oracle_fp64(c, keep), f"prefill nan rows {layout}")
