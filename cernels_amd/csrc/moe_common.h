@@ -120,6 +120,20 @@ __device__ __forceinline__ f32x4 unpack_f24x4(const f24x4& p) {
                  f24_to_f32((p.d[1] >> 16) | ((p.d[2] & 0xffu) << 16)), f24_to_f32(p.d[2] >> 8)};
 }
 
+// Half-wave exchange (v_permlane32_swap_b32): lanes 32..63 of a and lanes 0..31 of b trade places, so lane l
+// of a afterwards holds b's lane l - 32 (l >= 32) and lane l of b holds a's lane l + 32 (l < 32).
+__device__ __forceinline__ void swap_halves(uint32_t& a, uint32_t& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+// The larger of lane l's and lane l ^ 32's values, in both lanes (fmaxf: a nan is passed over).
+__device__ __forceinline__ float max_halves(float v) {
+    uint32_t a = __float_as_uint(v), b = a;
+    swap_halves(a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+
 // Full-wave (64-lane) maximum; every lane returns it.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -675,7 +675,13 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
         // block, column 8*(r/4) + 4*(lane/32) + (r%4) of the fragment. Only LDS reads and global
         // stores here: a global load would have to wait for the next item's weights in flight.
         if (active) {
-            const int c4 = 4 * (lane >> 5);
+            // lane & 31 and lane >> 5 rebuilt here from v_mbcnt (no inputs; in asm, so not hoisted): from the lane
+            // register, the rows mb * 32 + (lane & 31) of all eight blocks were computed once before the item loop
+            // and held through the k-loops or spilled (and then reloaded here behind the next item's loads).
+            int lid;
+            asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lid));
+            const int lrow = lid & 31, half = lid >> 5;
+            const int c4 = 4 * half;
             // glu stores: fp16 segments (16 columns per lane pair for gate_up, 32 for the non-gated
             // projection), each with its power of two s in gexp: 0, unless the segment's largest |glu| m
             // is 2^15 or more (or not finite) or below 2^-8 (and not 0); then the segment is stored
@@ -690,7 +696,7 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                 return m < 32768.f ? max(-126, s) : max(1, s);
             };
             auto mark_scaled = [&](long long r) {
-                if (lane < 32) prm.rsig[r] = 1;
+                if (half == 0) prm.rsig[r] = 1;
                 prm.sync[1] = 1;
             };
             if constexpr (MODE == kModePkGateUp) {
@@ -712,54 +718,77 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                         v[jj] = swiglu<ACT>(gv, uv);
                     }
                 };
+                // A lane holds glu columns c4 + 0..3 and c4 + 8..11 of the fragment's 16: one exchange between the
+                // half-waves (columns 8-11 of lane l for 4-7 of lane l + 32) leaves lane l columns 0-7 and lane
+                // l + 32 columns 8-15, one 16-byte store each. h: the two groups, two packed dwords each.
+                auto store_glu = [&](uint16_t* g, uint32_t (&h)[4]) {
+                    swap_halves(h[0], h[2]);
+                    swap_halves(h[1], h[3]);
+                    *reinterpret_cast<u32x4*>(g) = u32x4{h[0], h[1], h[2], h[3]};
+                };
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
-                    const int row = mb * 32 + (lane & 31);
-                    if (row < rows) {  // lanes l and l ^ 32 hold the same row
+                    const int row = mb * 32 + lrow;
+                    if (row < rows) {  // lanes l and l ^ 32 hold the same row, so both run this or neither
                         const long long r = row_begin + row;
-                        uint16_t* g = glu + r * prm.F + 16 * fc + c4;
+                        uint16_t* g = glu + r * prm.F + 16 * fc + 8 * half;
                         // the segment's largest |glu|; a nan is passed over (it reaches the output as a nan
                         // at any scale), an inf is not (scaled down, it keeps finite values finite)
                         float m = 0.f;
+                        uint32_t h[4];
 #pragma unroll
                         for (int i = 0; i < 2; ++i) {
                             float v[4];
                             glu4(mb, i, v);
 #pragma unroll
                             for (int jj = 0; jj < 4; ++jj) m = fmaxf(m, fabsf(v[jj]));
-                            *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+                            h[2 * i] = pack_f16x2(v[0], v[1]);
+                            h[2 * i + 1] = pack_f16x2(v[2], v[3]);
                         }
-                        m = fmaxf(m, __shfl_xor(m, 32, kWave));  // the same on both lanes of the row
-                        if (lane < 32) prm.gexp[(long long)fc * prm.p_cap + r] = (int8_t)(m == 0.f ? kGluAnyScale : 0);
-                        if (needs_scale(m)) {  // rare: store the segment scaled
-                            float v[2][4];
-#pragma unroll
-                            for (int i = 0; i < 2; ++i) glu4(mb, i, v[i]);
+                        store_glu(g, h);
+                        m = max_halves(m);  // the same on both lanes of the row
+                        if (half == 0) prm.gexp[(long long)fc * prm.p_cap + r] = (int8_t)(m == 0.f ? kGluAnyScale : 0);
+                        if (needs_scale(m)) {  // rare: the segment stored again, scaled, by the same lanes
                             const int sg = glu_scale(m);
 #pragma unroll
-                            for (int i = 0; i < 2; ++i)
-                                *reinterpret_cast<u32x2*>(g + 8 * i) =
-                                    u32x2{pack_f16x2(__builtin_amdgcn_ldexpf(v[i][0], -sg), __builtin_amdgcn_ldexpf(v[i][1], -sg)),
-                                          pack_f16x2(__builtin_amdgcn_ldexpf(v[i][2], -sg), __builtin_amdgcn_ldexpf(v[i][3], -sg))};
-                            if (lane < 32) prm.gexp[(long long)fc * prm.p_cap + r] = (int8_t)sg;
+                            for (int i = 0; i < 2; ++i) {
+                                float v[4];
+                                glu4(mb, i, v);
+                                h[2 * i] = pack_f16x2(__builtin_amdgcn_ldexpf(v[0], -sg), __builtin_amdgcn_ldexpf(v[1], -sg));
+                                h[2 * i + 1] = pack_f16x2(__builtin_amdgcn_ldexpf(v[2], -sg), __builtin_amdgcn_ldexpf(v[3], -sg));
+                            }
+                            store_glu(g, h);
+                            if (half == 0) prm.gexp[(long long)fc * prm.p_cap + r] = (int8_t)sg;
                             mark_scaled(r);
                         }
                     }
                 }
             } else if constexpr (MODE == kModePkUp) {
                 // 16 columns of the fragment per lane (8i + c4 + jj), activation, fp16 glu row segment of
-                // 32 columns (two gexp entries).
+                // 32 columns (two gexp entries). Two exchanges between the half-waves (groups i = 0, 1 of lane
+                // l + 32 for groups 2, 3 of lane l) leave lane l columns 0-15 and lane l + 32 columns 16-31, two
+                // 16-byte stores each. s: the segment's scale (0: none).
+                auto store_glu = [&](uint16_t* g, uint32_t (&h)[4][2]) {
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        swap_halves(h[0][d], h[2][d]);
+                        swap_halves(h[1][d], h[3][d]);
+                    }
+                    *reinterpret_cast<u32x4*>(g) = u32x4{h[0][0], h[0][1], h[2][0], h[2][1]};
+                    *reinterpret_cast<u32x4*>(g + 8) = u32x4{h[1][0], h[1][1], h[3][0], h[3][1]};
+                };
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
-                    const int row = mb * 32 + (lane & 31);
-                    if (row < rows) {  // lanes l and l ^ 32 hold the same row
+                    const int row = mb * 32 + lrow;
+                    if (row < rows) {  // lanes l and l ^ 32 hold the same row, so both run this or neither
                         const long long r = row_begin + row;
-                        uint16_t* g = glu + r * prm.F + 32 * fc + c4;
+                        uint16_t* g = glu + r * prm.F + 32 * fc + 16 * half;
                         // the segment's largest |glu|; a nan is passed over (it reaches the output as a nan
                         // at any scale), an inf is not (scaled down, it keeps finite values finite)
                         float m = 0.f;
+                        uint32_t h[4][2];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             float v[4];
@@ -768,15 +797,17 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                                 v[jj] = act_plain<ACT>(acc[mb][4 * i + jj]);
                                 m = fmaxf(m, fabsf(v[jj]));
                             }
-                            *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+                            h[i][0] = pack_f16x2(v[0], v[1]);
+                            h[i][1] = pack_f16x2(v[2], v[3]);
                         }
-                        m = fmaxf(m, __shfl_xor(m, 32, kWave));  // the same on both lanes of the row
-                        if (lane < 32) {
+                        store_glu(g, h);
+                        m = max_halves(m);  // the same on both lanes of the row
+                        if (half == 0) {
                             const int8_t s0 = (int8_t)(m == 0.f ? kGluAnyScale : 0);
                             prm.gexp[(long long)(2 * fc) * prm.p_cap + r] = s0;
                             prm.gexp[(long long)(2 * fc + 1) * prm.p_cap + r] = s0;
                         }
-                        if (needs_scale(m)) {  // rare: store the segment scaled
+                        if (needs_scale(m)) {  // rare: the segment stored again, scaled, by the same lanes
                             const int sg = glu_scale(m);
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
@@ -784,9 +815,11 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
 #pragma unroll
                                 for (int jj = 0; jj < 4; ++jj)
                                     v[jj] = __builtin_amdgcn_ldexpf(act_plain<ACT>(acc[mb][4 * i + jj]), -sg);
-                                *reinterpret_cast<u32x2*>(g + 8 * i) = u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
+                                h[i][0] = pack_f16x2(v[0], v[1]);
+                                h[i][1] = pack_f16x2(v[2], v[3]);
                             }
-                            if (lane < 32) {
+                            store_glu(g, h);
+                            if (half == 0) {
                                 prm.gexp[(long long)(2 * fc) * prm.p_cap + r] = (int8_t)sg;
                                 prm.gexp[(long long)(2 * fc + 1) * prm.p_cap + r] = (int8_t)sg;
                             }
@@ -795,29 +828,35 @@ __global__ __launch_bounds__(kPkThreads, 1) void moe_gemm_packed_kernel(PkParams
                     }
                 }
             } else {
-                // Y rows as 24-bit floats (fp32 rounded to 16 mantissa bits, 2^-16 relative), four
-                // consecutive columns per 12-byte store: the combine sums the K rows of a token from
-                // nearly exact values, at 3/4 of fp32's bytes.
+                // Y rows as 24-bit floats (fp32 rounded to 16 mantissa bits, 2^-16 relative): the combine sums
+                // the K rows of a token from nearly exact values, at 3/4 of fp32's bytes. A lane packs its four
+                // groups of four columns (8i + c4 + jj) into 12 bytes each; exchanging groups 0, 1 of lane
+                // l + 32 for groups 2, 3 of lane l (three dwords each) leaves lane l columns 0-15 of the row
+                // and lane l + 32 columns 16-31, 48 contiguous bytes each: three 16-byte stores (aligned: H is
+                // a multiple of 64) instead of four 12-byte ones.
                 unsigned char* Yb = reinterpret_cast<unsigned char*>(prm.out);
                 const float wsc = __builtin_amdgcn_ldexpf(1.0f, s_wx[tb][wave]);  // the fragment's fp16 scale
 #pragma unroll
                 for (int mb = 0; mb < kPkMB; ++mb) {
                     if (mb >= nmb) break;
-                    const int row = mb * 32 + (lane & 31);
-                    if (row < rows) {
+                    const int row = mb * 32 + lrow;
+                    if (row < rows) {  // lanes l and l ^ 32 hold the same row, so both run this or neither
                         const float ws = wsc * s_w[tb][row];  // exact: wsc is a power of two
                         const long long p = s_pair[tb][row];
-                        // this lane's first four columns of the row; the other three groups are 24, 48 and 72
-                        // bytes further (the stores' immediate offsets: one address per row, not per store)
-                        unsigned char* yrow = Yb + (p * prm.H + 32 * fc + c4) * 3;
+                        f24x4 q[4];
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            float a[4];
+                        for (int i = 0; i < 4; ++i)
+                            q[i] = pack_f24x4(acc[mb][4 * i] * ws, acc[mb][4 * i + 1] * ws, acc[mb][4 * i + 2] * ws,
+                                              acc[mb][4 * i + 3] * ws);
 #pragma unroll
-                            for (int jj = 0; jj < 4; ++jj) a[jj] = acc[mb][4 * i + jj] * ws;
-                            const f24x4 q = pack_f24x4(a[0], a[1], a[2], a[3]);
-                            __builtin_memcpy(yrow + 24 * i, &q, 12);
+                        for (int d = 0; d < 3; ++d) {
+                            swap_halves(q[0].d[d], q[2].d[d]);
+                            swap_halves(q[1].d[d], q[3].d[d]);
                         }
+                        u32x4* yrow = reinterpret_cast<u32x4*>(Yb + (p * prm.H + 32 * fc + 16 * half) * 3);
+                        yrow[0] = u32x4{q[0].d[0], q[0].d[1], q[0].d[2], q[2].d[0]};
+                        yrow[1] = u32x4{q[2].d[1], q[2].d[2], q[1].d[0], q[1].d[1]};
+                        yrow[2] = u32x4{q[1].d[2], q[3].d[0], q[3].d[1], q[3].d[2]};
                     }
                 }
             }
