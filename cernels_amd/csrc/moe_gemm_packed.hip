@@ -22,7 +22,10 @@
 // three weight register slots: both operands of a stage are requested two stages before its MFMAs.
 //
 // GEMM1 fragments hold 16 gate and the 16 matching up columns, so one wave holds both inputs of the
-// gated activation for its 16 glu columns; a v_permlane16_swap pairs them up in the epilogue.
+// gated activation for its 16 glu columns: elements r and r + 8 of a lane's accumulator block are gate
+// and up of the same glu column, and the activation runs in registers. In both epilogues lanes l and
+// l + 32 hold alternate groups of four columns of one row; a v_permlane32_swap per dword trades groups
+// between the half-waves so that each lane stores one contiguous run with 16-byte stores.
 //
 // Precision of the second projection. glu (the activation output, GEMM2's A operand) is stored as
 // fp16, not bf16: 2^-11 relative rounding instead of 2^-8, which is what keeps the output within
