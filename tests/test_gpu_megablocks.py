@@ -9,6 +9,8 @@ experts' tolerance, |out - fp64| <= 2e-2 RMS + half a bf16 ulp elementwise; the 
 
 from __future__ import annotations
 
+import random
+
 import pytest
 import torch
 
@@ -40,6 +42,23 @@ CASES = [
     (4, 1200, 192, 256, 8, 2, 1, 17),
     (5, 90, 320, 64, 3, 1, 2, 3),
 ]
+
+
+def _sweep(n=12, seed=20261204):
+    """Seeded random legal shapes (H, F any multiple of 64 up to 768, 1-16 experts, top-1..4, 1-700 tokens, each
+    activation, a few invalid ids): the same list on every run."""
+    r = random.Random(seed)
+    out = []
+    for i in range(n):
+        E = r.randint(1, 16)
+        K = r.randint(1, min(E, 4))
+        T = r.randint(1, 700)
+        out.append((3000 + i, T, 64 * r.randint(1, 12), 64 * r.randint(1, 12), E, K, i % 3,
+                    r.randint(0, 3) if T * K > 3 else 0))
+    return out
+
+
+CASES += _sweep()
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"T{c[1]}H{c[2]}F{c[3]}E{c[4]}k{c[5]}a{c[6]}")
